@@ -1,0 +1,206 @@
+/* nutllm_hip.h — C ABI of the MI355X (gfx950) token loop.
+ *
+ * This is the drop-in boundary under nutllm's C++17 host API: the
+ * generate_tokens_cached / prefill_quantized / decode_quantized_token /
+ * matvec_quantized_threaded entry points call these functions instead of the
+ * reference's CPU kernels. Every function returns a status (never throws);
+ * the status names the exception type the reference would have thrown, and
+ * nut_last_error() gives its message ("quantized decode: token out of
+ * range", ...). Citations are MokiMeow/nutllm path:line.
+ *
+ * Pointers named d_* are device pointers; all others are host pointers.
+ * One host thread drives a handle at a time (the reference serialises calls
+ * the same way, src/threading.cpp:50).
+ */
+#ifndef NUTLLM_HIP_H
+#define NUTLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status -- */
+
+enum {
+    NUT_OK = 0,
+    NUT_EINVAL = 1,      /* std::invalid_argument */
+    NUT_EOUTOFRANGE = 2, /* std::out_of_range */
+    NUT_ELENGTH = 3,     /* std::length_error */
+    NUT_ERANGE = 4,      /* std::range_error */
+    NUT_ERUNTIME = 5,    /* std::runtime_error */
+    NUT_EDEVICE = 6      /* HIP runtime error or no gfx950 device */
+};
+
+/* Message of the last failing call on this thread ("" after success). */
+const char *nut_last_error(void);
+
+/* ------------------------------------------------------------- types -- */
+
+/* QuantType (include/quant.hpp:9-12). */
+enum { NUT_INT8 = 0, NUT_INT4 = 1 };
+
+/* ModelConfig (include/model.hpp:8-24); kv_heads == 0 means heads. */
+typedef struct nut_config {
+    size_t layers, heads, dim, head_dim, ffn_dim, vocab_size, max_seq,
+        eos_token, kv_heads;
+} nut_config;
+
+/* Host view of a QuantizedMatrix's storage (include/quant.hpp:40-49):
+ * flattened row-major blocks of block_size weights; INT8 bytes or INT4
+ * nibbles (even flattened index in the low nibble), fp16 scale bits. */
+typedef struct nut_qmatrix {
+    const uint8_t *data;
+    const uint16_t *scales;
+    size_t rows, cols, block_size;
+    int type;
+} nut_qmatrix;
+
+/* GenerationStats (include/generate.hpp:19-24). */
+typedef struct nut_generation_stats {
+    size_t prefill_tokens, generated_tokens;
+    double prefill_seconds, decode_seconds;
+} nut_generation_stats;
+
+/* ------------------------------------------- host utilities (no GPU) -- */
+
+/* QuantizedMatrix::quantize (src/quant.cpp:154-197), bit-exact: data gets
+ * nut_quant_data_bytes bytes, scales nut_quant_scale_count fp16 words.
+ * NUT_EINVAL on non-finite weights or bad shape, NUT_ERANGE when a scale
+ * exceeds fp16 (src/quant.cpp:24-27,44-45). Runs on host threads. */
+int nut_quantize(const float *source, size_t rows, size_t cols, int type,
+                 size_t block_size, uint8_t *data, uint16_t *scales);
+size_t nut_quant_data_bytes(size_t rows, size_t cols, int type);
+size_t nut_quant_scale_count(size_t rows, size_t cols, size_t block_size);
+/* QuantizedMatrix::storage_bytes (src/quant.cpp:235-241). */
+size_t nut_quant_storage_bytes(size_t rows, size_t cols, int type,
+                               size_t block_size);
+/* positive_float_to_half / positive_half_to_float (src/quant.cpp:23-56). */
+int nut_float_to_half(float value, uint16_t *bits);
+float nut_half_to_float(uint16_t bits);
+/* ModelConfig::validate (src/attention.cpp:15-27): 1 when valid. */
+int nut_config_valid(const nut_config *config);
+
+/* Synthetic workload generator (no reference counterpart: the reference
+ * loads checkpoints). N(0, sigma^2) fp32 values from a counter-based
+ * splitmix64 + Box-Muller stream keyed by (seed, stream); element i depends
+ * only on (seed, stream, i), so any thread count gives the same array. */
+int nut_synth_normal(uint64_t seed, uint64_t stream, float sigma, float *out,
+                     size_t count);
+/* Uniform token ids in [0, vocab) (rejection sampled) from seed. */
+int nut_synth_tokens(uint64_t seed, size_t vocab, int *out, size_t count);
+
+/* ------------------------------------------------- device and memory -- */
+
+/* Number of visible gfx950 devices (0 on a host without a GPU). */
+int nut_device_count(int *count);
+/* Select the device this thread's calls use (default 0). */
+int nut_set_device(int device);
+int nut_malloc(void **d_ptr, size_t bytes);
+int nut_free(void *d_ptr);
+int nut_memcpy_h2d(void *d_dst, const void *src, size_t bytes);
+int nut_memcpy_d2h(void *dst, const void *d_src, size_t bytes);
+int nut_memset(void *d_dst, int value, size_t bytes);
+int nut_synchronize(void);
+
+/* --------------------------------------------- standalone kernels -- */
+
+/* A QuantizedMatrix uploaded to HBM (weights verbatim, fp16 scales). */
+typedef struct nut_qweight nut_qweight;
+int nut_qweight_create(const nut_qmatrix *host, nut_qweight **out);
+int nut_qweight_destroy(nut_qweight *w);
+size_t nut_qweight_device_bytes(const nut_qweight *w);
+
+/* y = W x on the device: matvec_quantized_threaded (src/quant.cpp:262-321).
+ * stream may be NULL (the null stream). */
+int nut_matvec_q(const nut_qweight *w, const float *d_x, float *d_y,
+                 void *stream);
+/* fp32 y = W x, W [rows x cols] row-major: matvec_threaded
+ * (src/threading.cpp:183-198), the classifier kernel. */
+int nut_matvec_f32(const float *d_w, size_t rows, size_t cols,
+                   const float *d_x, float *d_y, void *stream);
+/* fp32 C = A B, row-major A [m x k], B [k x n]: matmul_threaded
+ * (src/threading.cpp:163-181). */
+int nut_matmul_f32(const float *d_a, const float *d_b, float *d_c, size_t m,
+                   size_t k, size_t n, void *stream);
+
+/* Launch-time of the last nut_matvec_q / nut_matvec_f32 / nut_matmul_f32
+ * batch measured with HIP events: call nut_timer_begin(stream), launch,
+ * then nut_timer_end(stream, &ms) waits and returns elapsed milliseconds on
+ * that stream. (No reference counterpart; the reference times with
+ * std::chrono around whole calls.) */
+int nut_timer_begin(void *stream);
+int nut_timer_end(void *stream, double *milliseconds);
+
+/* ------------------------------------------------------------- model -- */
+
+typedef struct nut_model nut_model;
+
+/* QuantizedModelWeights (include/quant_model.hpp:32-46): validates config,
+ * allocates device storage for every layer; tied selects embeddings as the
+ * classifier (output_weights(), include/quant_model.hpp:42-44). */
+int nut_model_create(const nut_config *config, int type, int tied,
+                     nut_model **out);
+/* fp32 embeddings [vocab x dim], final_norm [dim], lm_head [vocab x dim]
+ * (ignored when tied). */
+int nut_model_set_globals(nut_model *m, const float *embeddings,
+                          const float *final_norm, const float *lm_head);
+/* QuantizedLayerWeights (include/quant_model.hpp:9-30): projections in
+ * [out x in] layout: query dim x dim, key/value kv_dim x dim, output
+ * dim x dim, gate/up ffn x dim, down dim x ffn. */
+int nut_model_set_layer(nut_model *m, size_t layer, const nut_qmatrix *query,
+                        const nut_qmatrix *key, const nut_qmatrix *value,
+                        const nut_qmatrix *output, const nut_qmatrix *gate,
+                        const nut_qmatrix *up, const nut_qmatrix *down,
+                        const float *attention_norm, const float *ffn_norm);
+/* QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156). */
+size_t nut_model_storage_bytes(const nut_model *m);
+int nut_model_destroy(nut_model *m);
+
+/* ---------------------------------------------------------- KV cache -- */
+
+/* KVCache (include/kvcache.hpp:8-31, src/kvcache.cpp:173-235): fp32 K and
+ * V in HBM, [layer][kv_head][position][head_dim]. */
+typedef struct nut_kvcache nut_kvcache;
+int nut_kv_create(const nut_config *config, nut_kvcache **out);
+int nut_kv_destroy(nut_kvcache *kv);
+size_t nut_kv_length(const nut_kvcache *kv);
+size_t nut_kv_capacity(const nut_kvcache *kv);
+size_t nut_kv_memory_bytes(const nut_kvcache *kv);
+int nut_kv_compatible(const nut_kvcache *kv, const nut_config *config);
+int nut_kv_reset(nut_kvcache *kv);
+int nut_kv_set_length(nut_kvcache *kv, size_t length);
+/* KVCache::key / value: copy one [head_dim] row to the host. */
+int nut_kv_read(const nut_kvcache *kv, size_t layer, size_t head,
+                size_t position, float *key, float *value);
+/* KVCache::store: key/value are [kv_heads x head_dim] host vectors. */
+int nut_kv_store(nut_kvcache *kv, size_t layer, size_t position,
+                 const float *key, const float *value);
+
+/* -------------------------------------------------------- token loop -- */
+
+/* decode_quantized_token (src/quant_model.cpp:158-206): one token through
+ * every layer at position = length; writes the pre-final-norm hidden state
+ * [dim] to hidden (host, may be NULL) and increments the length. */
+int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden);
+/* prefill_quantized (src/quant_model.cpp:208-220): resets the cache and
+ * runs the prompt; hidden gets the last token's hidden state. */
+int nut_prefill(nut_model *m, nut_kvcache *kv, const int *tokens,
+                size_t count, float *hidden);
+/* Final rmsnorm + fp32 classifier (src/generate.cpp:197-200) on a host
+ * hidden state; logits [vocab] to the host. */
+int nut_logits(nut_model *m, const float *hidden, float *logits);
+/* Greedy generate_tokens_cached (src/generate.cpp:174-216) with its
+ * GenerationStats timing; out receives up to max_tokens ids, stopping at
+ * eos_token or a full cache. The loop runs on the device: the argmax of
+ * each step feeds the next step without a host round trip. */
+int nut_generate_greedy(nut_model *m, const int *prompt, size_t prompt_len,
+                        size_t max_tokens, int *out, size_t *out_count,
+                        nut_generation_stats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

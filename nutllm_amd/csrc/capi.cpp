@@ -1,0 +1,401 @@
+// capi.cpp — the extern "C" entry points declared in include/nutllm_hip.h.
+// Each one validates its arguments, runs under nut::guarded (exceptions
+// become status codes plus nut_last_error()), and forwards to the runtime.
+#include <cstring>
+#include <unordered_map>
+
+#include "kernels.hpp"
+#include "model.hpp"
+
+namespace nut {
+int select_device(int device);
+const char *last_error();
+} // namespace nut
+
+struct nut_qweight {
+    nut::DeviceBuffer data, scales;
+    nut::QMat view{};
+    size_t device_bytes = 0;
+};
+
+namespace {
+
+hipStream_t as_stream(void *stream) { return static_cast<hipStream_t>(stream); }
+
+struct TimerPair {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+
+thread_local std::unordered_map<void *, TimerPair> g_timers;
+
+} // namespace
+
+extern "C" {
+
+const char *nut_last_error(void) { return nut::last_error(); }
+
+int nut_config_valid(const nut_config *config)
+{
+    return config != nullptr && nut::config_valid(*config) ? 1 : 0;
+}
+
+int nut_device_count(int *count)
+{
+    return nut::guarded([&]() {
+        nut::require(count != nullptr, NUT_EINVAL, "device count: null output");
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess)
+            n = 0;
+        int gfx950 = 0;
+        for (int d = 0; d < n; d++) {
+            hipDeviceProp_t props;
+            if (hipGetDeviceProperties(&props, d) == hipSuccess &&
+                std::strncmp(props.gcnArchName, "gfx950", 6) == 0)
+                gfx950++;
+        }
+        *count = gfx950;
+    });
+}
+
+int nut_set_device(int device)
+{
+    return nut::guarded([&]() { nut::select_device(device); });
+}
+
+int nut_malloc(void **d_ptr, size_t bytes)
+{
+    return nut::guarded([&]() {
+        nut::require(d_ptr != nullptr, NUT_EINVAL, "malloc: null output");
+        nut::ensure_device();
+        nut::hip_check(hipMalloc(d_ptr, bytes == 0 ? 1 : bytes), "hipMalloc");
+    });
+}
+
+int nut_free(void *d_ptr)
+{
+    return nut::guarded([&]() {
+        if (d_ptr != nullptr)
+            nut::hip_check(hipFree(d_ptr), "hipFree");
+    });
+}
+
+int nut_memcpy_h2d(void *d_dst, const void *src, size_t bytes)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        nut::hip_check(hipMemcpy(d_dst, src, bytes, hipMemcpyHostToDevice),
+                       "hipMemcpy to device");
+    });
+}
+
+int nut_memcpy_d2h(void *dst, const void *d_src, size_t bytes)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        nut::hip_check(hipMemcpy(dst, d_src, bytes, hipMemcpyDeviceToHost),
+                       "hipMemcpy to host");
+    });
+}
+
+int nut_memset(void *d_dst, int value, size_t bytes)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        nut::hip_check(hipMemset(d_dst, value, bytes), "hipMemset");
+    });
+}
+
+int nut_synchronize(void)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        nut::hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    });
+}
+
+int nut_qweight_create(const nut_qmatrix *host, nut_qweight **out)
+{
+    return nut::guarded([&]() {
+        nut::require(host != nullptr && out != nullptr && host->data != nullptr &&
+                         host->scales != nullptr,
+                     NUT_EINVAL, "quantized matvec: null pointer");
+        nut::require(host->rows != 0 && host->cols != 0 && host->block_size != 0 &&
+                         host->rows <= 0x7fffffff && host->cols <= 0x7fffffff,
+                     NUT_EINVAL, "quantize: invalid dimensions");
+        nut::require(host->type == NUT_INT8 || host->type == NUT_INT4, NUT_EINVAL,
+                     "quantize: unknown quant type");
+        nut::ensure_device();
+        std::unique_ptr<nut_qweight> w(new nut_qweight());
+        const size_t data = nut_quant_data_bytes(host->rows, host->cols, host->type);
+        const size_t scales =
+            2 * nut_quant_scale_count(host->rows, host->cols, host->block_size);
+        w->data.allocate(data);
+        w->scales.allocate(scales);
+        nut::hip_check(hipMemcpy(w->data.get(), host->data, data, hipMemcpyHostToDevice),
+                       "hipMemcpy to device");
+        nut::hip_check(hipMemcpy(w->scales.get(), host->scales, scales,
+                                 hipMemcpyHostToDevice),
+                       "hipMemcpy to device");
+        w->view = nut::QMat{w->data.as<uint8_t>(), w->scales.as<uint16_t>(),
+                            int(host->rows), int(host->cols), int(host->block_size),
+                            host->type};
+        w->device_bytes = data + scales;
+        *out = w.release();
+    });
+}
+
+int nut_qweight_destroy(nut_qweight *w)
+{
+    return nut::guarded([&]() { delete w; });
+}
+
+size_t nut_qweight_device_bytes(const nut_qweight *w)
+{
+    return w == nullptr ? 0 : w->device_bytes;
+}
+
+int nut_matvec_q(const nut_qweight *w, const float *d_x, float *d_y, void *stream)
+{
+    return nut::guarded([&]() {
+        nut::require(w != nullptr && d_x != nullptr && d_y != nullptr, NUT_EINVAL,
+                     "quantized matvec: null pointer");
+        nut::ensure_device();
+        nut::launch_matvec_q(w->view, d_x, d_y, as_stream(stream));
+    });
+}
+
+int nut_matvec_f32(const float *d_w, size_t rows, size_t cols, const float *d_x,
+                   float *d_y, void *stream)
+{
+    return nut::guarded([&]() {
+        nut::require(d_w != nullptr && d_x != nullptr && d_y != nullptr, NUT_EINVAL,
+                     "threaded matvec: null pointer");
+        nut::require(rows != 0 && cols != 0 && rows <= 0x7fffffff && cols <= 0x7fffffff,
+                     NUT_EINVAL, "threaded kernel: zero rows");
+        nut::ensure_device();
+        nut::launch_matvec_f32(d_w, int(rows), int(cols), d_x, d_y, as_stream(stream));
+    });
+}
+
+int nut_matmul_f32(const float *d_a, const float *d_b, float *d_c, size_t m, size_t k,
+                   size_t n, void *stream)
+{
+    return nut::guarded([&]() {
+        nut::require(d_a != nullptr && d_b != nullptr && d_c != nullptr, NUT_EINVAL,
+                     "threaded matmul: null pointer");
+        nut::require(m != 0 && k != 0 && n != 0 && m <= 0x7fffffff && k <= 0x7fffffff &&
+                         n <= 0x7fffffff,
+                     NUT_EINVAL, "threaded matmul: shape mismatch");
+        nut::ensure_device();
+        nut::launch_matmul_f32(d_a, d_b, d_c, int(m), int(k), int(n), as_stream(stream));
+    });
+}
+
+int nut_timer_begin(void *stream)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        TimerPair &t = g_timers[stream];
+        if (t.start == nullptr) {
+            nut::hip_check(hipEventCreate(&t.start), "hipEventCreate");
+            nut::hip_check(hipEventCreate(&t.stop), "hipEventCreate");
+        }
+        nut::hip_check(hipEventRecord(t.start, as_stream(stream)), "hipEventRecord");
+    });
+}
+
+int nut_timer_end(void *stream, double *milliseconds)
+{
+    return nut::guarded([&]() {
+        nut::require(milliseconds != nullptr, NUT_EINVAL, "timer: null output");
+        auto it = g_timers.find(stream);
+        nut::require(it != g_timers.end(), NUT_EINVAL, "timer: not started");
+        nut::hip_check(hipEventRecord(it->second.stop, as_stream(stream)),
+                       "hipEventRecord");
+        nut::hip_check(hipEventSynchronize(it->second.stop), "hipEventSynchronize");
+        float ms = 0.0f;
+        nut::hip_check(hipEventElapsedTime(&ms, it->second.start, it->second.stop),
+                       "hipEventElapsedTime");
+        *milliseconds = ms;
+    });
+}
+
+int nut_model_create(const nut_config *config, int type, int tied, nut_model **out)
+{
+    return nut::guarded([&]() {
+        nut::require(config != nullptr && out != nullptr, NUT_EINVAL,
+                     "quantized model: null pointer");
+        *out = nut::create_model(*config, type, tied != 0);
+    });
+}
+
+int nut_model_set_globals(nut_model *m, const float *embeddings, const float *final_norm,
+                          const float *lm_head)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::ensure_device();
+        nut::set_globals(*m, embeddings, final_norm, lm_head);
+    });
+}
+
+int nut_model_set_layer(nut_model *m, size_t layer, const nut_qmatrix *query,
+                        const nut_qmatrix *key, const nut_qmatrix *value,
+                        const nut_qmatrix *output, const nut_qmatrix *gate,
+                        const nut_qmatrix *up, const nut_qmatrix *down,
+                        const float *attention_norm, const float *ffn_norm)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::ensure_device();
+        const nut_qmatrix *mats[7] = {query, key, value, output, gate, up, down};
+        nut::set_layer(*m, layer, mats, attention_norm, ffn_norm);
+    });
+}
+
+size_t nut_model_storage_bytes(const nut_model *m)
+{
+    return m == nullptr ? 0 : nut::storage_bytes(*m);
+}
+
+int nut_model_destroy(nut_model *m)
+{
+    return nut::guarded([&]() { delete m; });
+}
+
+int nut_kv_create(const nut_config *config, nut_kvcache **out)
+{
+    return nut::guarded([&]() {
+        nut::require(config != nullptr && out != nullptr, NUT_EINVAL,
+                     "kv cache: null pointer");
+        *out = nut::create_kv(*config);
+    });
+}
+
+int nut_kv_destroy(nut_kvcache *kv)
+{
+    return nut::guarded([&]() { delete kv; });
+}
+
+size_t nut_kv_length(const nut_kvcache *kv) { return kv == nullptr ? 0 : kv->length; }
+
+size_t nut_kv_capacity(const nut_kvcache *kv) { return kv == nullptr ? 0 : kv->config.max_seq; }
+
+size_t nut_kv_memory_bytes(const nut_kvcache *kv)
+{
+    // KVCache::memory_bytes (src/kvcache.cpp:179-185): keys + values.
+    return kv == nullptr ? 0 : 2 * kv->config.layers * kv->layer_elements() * sizeof(float);
+}
+
+int nut_kv_compatible(const nut_kvcache *kv, const nut_config *config)
+{
+    return kv != nullptr && config != nullptr && nut::kv_compatible(*kv, *config) ? 1 : 0;
+}
+
+int nut_kv_reset(nut_kvcache *kv)
+{
+    return nut::guarded([&]() {
+        nut::require(kv != nullptr, NUT_EINVAL, "kv cache: null cache");
+        kv->length = 0;
+    });
+}
+
+int nut_kv_set_length(nut_kvcache *kv, size_t length)
+{
+    return nut::guarded([&]() {
+        nut::require(kv != nullptr, NUT_EINVAL, "kv cache: null cache");
+        nut::require(length <= kv->config.max_seq, NUT_ELENGTH,
+                     "kv cache: context exceeds capacity");
+        kv->length = length;
+    });
+}
+
+int nut_kv_read(const nut_kvcache *kv, size_t layer, size_t head, size_t position,
+                float *key, float *value)
+{
+    return nut::guarded([&]() {
+        nut::require(kv != nullptr, NUT_EINVAL, "kv cache: null cache");
+        nut::require(layer < kv->config.layers && head < kv->kv_heads() &&
+                         position < kv->config.max_seq,
+                     NUT_EOUTOFRANGE, "kv cache: index out of range");
+        nut::ensure_device();
+        const size_t hd = kv->config.head_dim;
+        const size_t offset =
+            layer * kv->layer_elements() + (head * kv->config.max_seq + position) * hd;
+        if (key != nullptr)
+            nut::hip_check(hipMemcpy(key, kv->keys.as<float>() + offset, hd * sizeof(float),
+                                     hipMemcpyDeviceToHost),
+                           "hipMemcpy to host");
+        if (value != nullptr)
+            nut::hip_check(hipMemcpy(value, kv->values.as<float>() + offset,
+                                     hd * sizeof(float), hipMemcpyDeviceToHost),
+                           "hipMemcpy to host");
+    });
+}
+
+int nut_kv_store(nut_kvcache *kv, size_t layer, size_t position, const float *key,
+                 const float *value)
+{
+    return nut::guarded([&]() {
+        nut::require(kv != nullptr, NUT_EINVAL, "kv cache: null cache");
+        nut::require(key != nullptr && value != nullptr, NUT_EINVAL,
+                     "kv cache: null source");
+        nut::require(layer < kv->config.layers && position < kv->config.max_seq,
+                     NUT_EOUTOFRANGE, "kv cache: index out of range");
+        nut::ensure_device();
+        const size_t hd = kv->config.head_dim;
+        for (size_t head = 0; head < kv->kv_heads(); head++) {
+            const size_t offset = layer * kv->layer_elements() +
+                                  (head * kv->config.max_seq + position) * hd;
+            nut::hip_check(hipMemcpy(kv->keys.as<float>() + offset, key + head * hd,
+                                     hd * sizeof(float), hipMemcpyHostToDevice),
+                           "hipMemcpy to device");
+            nut::hip_check(hipMemcpy(kv->values.as<float>() + offset, value + head * hd,
+                                     hd * sizeof(float), hipMemcpyHostToDevice),
+                           "hipMemcpy to device");
+        }
+    });
+}
+
+int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && kv != nullptr, NUT_EINVAL,
+                     "quantized decode: null pointer");
+        nut::ensure_device();
+        nut::decode(*m, *kv, token, hidden);
+    });
+}
+
+int nut_prefill(nut_model *m, nut_kvcache *kv, const int *tokens, size_t count,
+                float *hidden)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && kv != nullptr, NUT_EINVAL,
+                     "quantized prefill: null pointer");
+        nut::ensure_device();
+        nut::prefill(*m, *kv, tokens, count, hidden);
+    });
+}
+
+int nut_logits(nut_model *m, const float *hidden, float *logits)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "logits: null model");
+        nut::ensure_device();
+        nut::logits(*m, hidden, logits);
+    });
+}
+
+int nut_generate_greedy(nut_model *m, const int *prompt, size_t prompt_len,
+                        size_t max_tokens, int *out, size_t *out_count,
+                        nut_generation_stats *stats)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "generation: null model");
+        nut::ensure_device();
+        nut::generate_greedy(*m, prompt, prompt_len, max_tokens, out, out_count, stats);
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,393 @@
+// model.cpp — upload of QuantizedModelWeights to HBM, the device KV cache
+// and the host side of the token loop (decode, prefill, logits, greedy
+// generation). Validation and messages follow the reference's exceptions
+// (src/quant_model.cpp:161-172,212-213; src/generate.cpp:177-181).
+#include "model.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+namespace nut {
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+size_t kv_heads_of(const nut_config &c)
+{
+    return c.kv_heads == 0 ? c.heads : c.kv_heads;
+}
+
+DecodeShape shape_of(const nut_config &c)
+{
+    DecodeShape s{};
+    s.dim = int(c.dim);
+    s.heads = int(c.heads);
+    s.kv_heads = int(kv_heads_of(c));
+    s.head_dim = int(c.head_dim);
+    s.ffn_dim = int(c.ffn_dim);
+    s.vocab = int(c.vocab_size);
+    s.max_seq = int(c.max_seq);
+    s.eos = int(c.eos_token);
+    s.attn_scale = 1.0f / std::sqrt(float(c.head_dim));
+    return s;
+}
+
+// cos/sin of rotate_vector (src/quant_model.cpp:26-37), computed exactly as
+// the reference does: double frequency 10000^(-pair/hd), double angle,
+// rounded to fp32. Entry [pos][pair/2] = (cos, sin).
+std::vector<float> rope_table(const nut_config &c)
+{
+    const size_t half = c.head_dim / 2;
+    std::vector<float> table(c.max_seq * half * 2);
+    for (size_t pos = 0; pos < c.max_seq; pos++)
+        for (size_t i = 0; i < half; i++) {
+            const double frequency =
+                std::pow(10000.0, -double(2 * i) / double(c.head_dim));
+            const double angle = double(pos) * frequency;
+            table[(pos * half + i) * 2] = float(std::cos(angle));
+            table[(pos * half + i) * 2 + 1] = float(std::sin(angle));
+        }
+    return table;
+}
+
+void upload(void *dst, const void *src, size_t bytes)
+{
+    hip_check(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice),
+              "hipMemcpy to device");
+}
+
+void check_ready(const nut_model &m, const char *who)
+{
+    if (!m.globals_set)
+        fail(NUT_EINVAL, std::string(who) + ": model weights not uploaded");
+    for (const DeviceLayer &l : m.layers)
+        if (!l.set)
+            fail(NUT_EINVAL, std::string(who) + ": layer count mismatch");
+}
+
+// Enqueue one decode step reading its token from token_ptr (device).
+void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
+{
+    const DecodeShape &s = m.shape;
+    StepState *state = m.state.as<StepState>();
+    launch_embed(s, m.embeddings.as<float>(), token_ptr, state,
+                 m.hidden.as<float>(), m.stream);
+    const size_t layer_elems = kv.layer_elements();
+    for (size_t l = 0; l < m.layers.size(); l++)
+        launch_layer(s, m.layers[l].view, m.rope.as<float2>(),
+                     kv.device_length.as<int>(),
+                     kv.keys.as<float>() + l * layer_elems,
+                     kv.values.as<float>() + l * layer_elems,
+                     m.hidden.as<float>(), m.query.as<float>(),
+                     m.context.as<float>(), m.act.as<float>(), state,
+                     m.stream);
+    launch_finish_step(state, kv.device_length.as<int>(), m.stream);
+}
+
+void sync(nut_model &m) { hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize"); }
+
+double now() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
+
+} // namespace
+
+bool config_valid(const nut_config &c)
+{
+    const size_t kv = kv_heads_of(c);
+    return c.layers != 0 && c.heads != 0 && c.dim != 0 && c.head_dim != 0 &&
+           c.ffn_dim != 0 && c.vocab_size != 0 && c.max_seq != 0 &&
+           c.heads <= SIZE_MAX / c.head_dim && c.heads * c.head_dim == c.dim &&
+           c.head_dim % 2 == 0 && c.eos_token < c.vocab_size && kv != 0 &&
+           kv <= c.heads && c.heads % kv == 0;
+}
+
+nut_model *create_model(const nut_config &config, int type, bool tied)
+{
+    require(config_valid(config), NUT_EINVAL, "model config: invalid dimensions");
+    require(type == NUT_INT8 || type == NUT_INT4, NUT_EINVAL,
+            "quantized model: unknown quant type");
+    // Device-path limits: float4 head rows, LDS staging of x and scores.
+    require(config.head_dim % 4 == 0 && config.head_dim <= 256 &&
+                config.dim <= 15000 && config.ffn_dim <= 15000 &&
+                config.max_seq <= 15000 && config.vocab_size <= 0x7fffffff,
+            NUT_EINVAL, "quantized model: shape exceeds device kernel limits");
+    ensure_device();
+    std::unique_ptr<nut_model> m(new nut_model());
+    m->config = config;
+    m->type = type;
+    m->tied = tied;
+    m->shape = shape_of(config);
+    m->layers.resize(config.layers);
+    const size_t dim = config.dim, vocab = config.vocab_size;
+    m->embeddings.allocate(vocab * dim * sizeof(float));
+    m->final_norm.allocate(dim * sizeof(float));
+    if (!tied)
+        m->lm_head.allocate(vocab * dim * sizeof(float));
+    const std::vector<float> rope = rope_table(config);
+    m->rope.allocate(rope.size() * sizeof(float));
+    upload(m->rope.get(), rope.data(), rope.size() * sizeof(float));
+    m->hidden.allocate(dim * sizeof(float));
+    m->scratch_hidden.allocate(dim * sizeof(float));
+    m->query.allocate(dim * sizeof(float));
+    m->context.allocate(dim * sizeof(float));
+    m->act.allocate(config.ffn_dim * sizeof(float));
+    m->logits.allocate(vocab * sizeof(float));
+    m->part_val.allocate(1024 * sizeof(float));
+    m->part_idx.allocate(1024 * sizeof(int));
+    m->state.allocate(sizeof(StepState));
+    m->tokens.allocate((config.max_seq + 1) * sizeof(int));
+    m->prompt.allocate((config.max_seq + 1) * sizeof(int));
+    hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking),
+              "hipStreamCreate");
+    return m.release();
+}
+
+void set_globals(nut_model &m, const float *embeddings,
+                 const float *final_norm, const float *lm_head)
+{
+    const size_t dim = m.config.dim, vocab = m.config.vocab_size;
+    require(embeddings != nullptr && final_norm != nullptr &&
+                (m.tied || lm_head != nullptr),
+            NUT_EINVAL, "quantized model: null weights");
+    upload(m.embeddings.get(), embeddings, vocab * dim * sizeof(float));
+    upload(m.final_norm.get(), final_norm, dim * sizeof(float));
+    if (!m.tied)
+        upload(m.lm_head.get(), lm_head, vocab * dim * sizeof(float));
+    m.globals_set = true;
+}
+
+void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
+               const float *attention_norm, const float *ffn_norm)
+{
+    const nut_config &c = m.config;
+    require(layer < c.layers, NUT_EOUTOFRANGE, "quantized model: layer out of range");
+    require(attention_norm != nullptr && ffn_norm != nullptr, NUT_EINVAL,
+            "quantized model: null norm weights");
+    const size_t kvd = kv_heads_of(c) * c.head_dim;
+    const size_t shapes[7][2] = {{c.dim, c.dim},     {kvd, c.dim},
+                                 {kvd, c.dim},       {c.dim, c.dim},
+                                 {c.ffn_dim, c.dim}, {c.ffn_dim, c.dim},
+                                 {c.dim, c.ffn_dim}};
+    size_t offsets[7][2];
+    size_t total = 0, accounted = 0;
+    for (int i = 0; i < 7; i++) {
+        const nut_qmatrix *q = mats[i];
+        require(q != nullptr && q->data != nullptr && q->scales != nullptr,
+                NUT_EINVAL, "quantized model: null projection");
+        require(q->rows == shapes[i][0] && q->cols == shapes[i][1],
+                NUT_EINVAL, "quantized model: projection shape mismatch");
+        require(q->type == m.type, NUT_EINVAL, "quantized model: quant type mismatch");
+        require(q->block_size != 0, NUT_EINVAL, "quantize: zero block size");
+        const size_t data = nut_quant_data_bytes(q->rows, q->cols, q->type);
+        const size_t scales = 2 * nut_quant_scale_count(q->rows, q->cols, q->block_size);
+        offsets[i][0] = total;
+        total = align_up(total + data);
+        offsets[i][1] = total;
+        total = align_up(total + scales);
+        accounted += data + scales;
+    }
+    const size_t norms = total;
+    total += 2 * c.dim * sizeof(float);
+    DeviceLayer &dl = m.layers[layer];
+    dl.storage.release();
+    dl.storage.allocate(total);
+    uint8_t *base = dl.storage.as<uint8_t>();
+    QMat views[7];
+    for (int i = 0; i < 7; i++) {
+        const nut_qmatrix *q = mats[i];
+        upload(base + offsets[i][0], q->data, nut_quant_data_bytes(q->rows, q->cols, q->type));
+        upload(base + offsets[i][1], q->scales,
+               2 * nut_quant_scale_count(q->rows, q->cols, q->block_size));
+        views[i] = QMat{base + offsets[i][0],
+                        reinterpret_cast<const uint16_t *>(base + offsets[i][1]),
+                        int(q->rows), int(q->cols), int(q->block_size), q->type};
+    }
+    float *norm_base = reinterpret_cast<float *>(base + norms);
+    upload(norm_base, attention_norm, c.dim * sizeof(float));
+    upload(norm_base + c.dim, ffn_norm, c.dim * sizeof(float));
+    dl.view = LayerView{views[0], views[1], views[2], views[3], views[4],
+                        views[5], views[6], norm_base, norm_base + c.dim};
+    dl.storage_bytes = accounted + 2 * c.dim * sizeof(float);
+    dl.set = true;
+}
+
+size_t storage_bytes(const nut_model &m)
+{
+    // QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156).
+    const size_t dim = m.config.dim, vocab = m.config.vocab_size;
+    size_t total = vocab * dim * 4 + dim * 4 + (m.tied ? 0 : vocab * dim * 4);
+    for (const DeviceLayer &l : m.layers)
+        total += l.storage_bytes;
+    return total;
+}
+
+nut_kvcache *create_kv(const nut_config &config)
+{
+    require(config_valid(config), NUT_EINVAL, "model config: invalid dimensions");
+    ensure_device();
+    std::unique_ptr<nut_kvcache> kv(new nut_kvcache());
+    kv->config = config;
+    const size_t bytes = config.layers * kv->layer_elements() * sizeof(float);
+    kv->keys.allocate(bytes);
+    kv->values.allocate(bytes);
+    hip_check(hipMemset(kv->keys.get(), 0, bytes), "hipMemset");
+    hip_check(hipMemset(kv->values.get(), 0, bytes), "hipMemset");
+    kv->device_length.allocate(sizeof(int));
+    hip_check(hipMemset(kv->device_length.get(), 0, sizeof(int)), "hipMemset");
+    return kv.release();
+}
+
+bool kv_compatible(const nut_kvcache &kv, const nut_config &c)
+{
+    // KVCache::compatible (src/kvcache.cpp:187-195).
+    const nut_config &k = kv.config;
+    return k.layers == c.layers && k.heads == c.heads && k.dim == c.dim &&
+           k.head_dim == c.head_dim && k.ffn_dim == c.ffn_dim &&
+           k.vocab_size == c.vocab_size && k.max_seq == c.max_seq &&
+           k.eos_token == c.eos_token && kv_heads_of(k) == kv_heads_of(c);
+}
+
+} // namespace nut
+
+void nut_kvcache::sync_length(hipStream_t stream)
+{
+    nut::launch_set_int(device_length.as<int>(), int(length), stream);
+}
+
+nut_model::~nut_model()
+{
+    if (stream != nullptr)
+        (void)hipStreamDestroy(stream);
+}
+
+namespace nut {
+
+void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden)
+{
+    require(config_valid(m.config), NUT_EINVAL, "model config: invalid dimensions");
+    require(kv_compatible(kv, m.config), NUT_EINVAL,
+            "quantized decode: cache configuration mismatch");
+    check_ready(m, "quantized decode");
+    require(token >= 0 && size_t(token) < m.config.vocab_size, NUT_EOUTOFRANGE,
+            "quantized decode: token out of range");
+    require(kv.length < kv.config.max_seq, NUT_ELENGTH,
+            "quantized decode: context is full");
+    kv.sync_length(m.stream);
+    launch_reset_state(m.state.as<StepState>(), token, m.stream);
+    enqueue_step(m, kv, &m.state.as<StepState>()->token);
+    if (hidden != nullptr)
+        hip_check(hipMemcpyAsync(hidden, m.hidden.get(), m.config.dim * sizeof(float),
+                                 hipMemcpyDeviceToHost, m.stream),
+                  "hipMemcpyAsync");
+    sync(m);
+    kv.length += 1;
+}
+
+void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
+             float *hidden)
+{
+    require(tokens != nullptr && count != 0 && count <= kv.config.max_seq,
+            NUT_EINVAL, "quantized prefill: invalid prompt");
+    require(config_valid(m.config), NUT_EINVAL, "model config: invalid dimensions");
+    require(kv_compatible(kv, m.config), NUT_EINVAL,
+            "quantized decode: cache configuration mismatch");
+    check_ready(m, "quantized decode");
+    kv.length = 0;
+    // The reference decodes token by token, so a bad id fails only when it
+    // is reached, with the valid prefix already in the cache.
+    size_t valid = 0;
+    while (valid < count && tokens[valid] >= 0 &&
+           size_t(tokens[valid]) < m.config.vocab_size)
+        valid++;
+    if (valid > 0) {
+        hip_check(hipMemcpyAsync(m.prompt.get(), tokens, valid * sizeof(int),
+                                 hipMemcpyHostToDevice, m.stream),
+                  "hipMemcpyAsync");
+        kv.sync_length(m.stream);
+        launch_reset_state(m.state.as<StepState>(), tokens[0], m.stream);
+        for (size_t t = 0; t < valid; t++)
+            enqueue_step(m, kv, m.prompt.as<int>() + t);
+        if (hidden != nullptr)
+            hip_check(hipMemcpyAsync(hidden, m.hidden.get(), m.config.dim * sizeof(float),
+                                     hipMemcpyDeviceToHost, m.stream),
+                      "hipMemcpyAsync");
+        sync(m);
+        kv.length = valid;
+    }
+    require(valid == count, NUT_EOUTOFRANGE, "quantized decode: token out of range");
+}
+
+void logits(nut_model &m, const float *hidden, float *out)
+{
+    require(hidden != nullptr && out != nullptr, NUT_EINVAL, "logits: null pointer");
+    check_ready(m, "logits");
+    const size_t dim = m.config.dim;
+    hip_check(hipMemcpyAsync(m.scratch_hidden.get(), hidden, dim * sizeof(float),
+                             hipMemcpyHostToDevice, m.stream),
+              "hipMemcpyAsync");
+    launch_reset_state(m.state.as<StepState>(), 0, m.stream);
+    launch_classifier(m.shape, m.scratch_hidden.as<float>(), m.final_norm.as<float>(),
+                      m.output_weights(), m.logits.as<float>(), m.part_val.as<float>(),
+                      m.part_idx.as<int>(), m.state.as<StepState>(), m.stream);
+    hip_check(hipMemcpyAsync(out, m.logits.get(), m.config.vocab_size * sizeof(float),
+                             hipMemcpyDeviceToHost, m.stream),
+              "hipMemcpyAsync");
+    sync(m);
+}
+
+void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
+                     size_t max_tokens, int *out, size_t *out_count,
+                     nut_generation_stats *stats)
+{
+    require(config_valid(m.config), NUT_EINVAL, "model config: invalid dimensions");
+    require(prompt != nullptr && prompt_len != 0 && prompt_len <= m.config.max_seq,
+            NUT_EINVAL, "generation: invalid prompt length");
+    require(out != nullptr || max_tokens == 0, NUT_EINVAL, "generation: null output");
+    require(out_count != nullptr, NUT_EINVAL, "generation: null output");
+    check_ready(m, "generation");
+    if (!m.generation_cache)
+        m.generation_cache.reset(create_kv(m.config));
+    nut_kvcache &kv = *m.generation_cache;
+
+    const double t0 = now();
+    prefill(m, kv, prompt, prompt_len, nullptr);
+    const double t1 = now();
+    const size_t steps = std::min(max_tokens, m.config.max_seq - prompt_len);
+    StepState *state = m.state.as<StepState>();
+    launch_reset_state(state, 0, m.stream);
+    const int parts = classifier_blocks(m.shape);
+    for (size_t i = 0; i < steps; i++) {
+        launch_classifier(m.shape, m.hidden.as<float>(), m.final_norm.as<float>(),
+                          m.output_weights(), nullptr, m.part_val.as<float>(),
+                          m.part_idx.as<int>(), state, m.stream);
+        launch_pick_token(m.shape, m.part_val.as<float>(), m.part_idx.as<int>(),
+                          parts, state, m.tokens.as<int>(), m.stream);
+        enqueue_step(m, kv, &state->token);
+    }
+    StepState host_state{};
+    hip_check(hipMemcpyAsync(&host_state, state, sizeof host_state,
+                             hipMemcpyDeviceToHost, m.stream),
+              "hipMemcpyAsync");
+    sync(m);
+    const double t2 = now();
+    const size_t count = size_t(host_state.count);
+    if (count > 0)
+        hip_check(hipMemcpy(out, m.tokens.get(), count * sizeof(int),
+                            hipMemcpyDeviceToHost),
+                  "hipMemcpy");
+    kv.length = prompt_len + count; // every emitted token was decoded
+    *out_count = count;
+    if (stats != nullptr) {
+        stats->prefill_tokens = prompt_len;
+        stats->generated_tokens = count;
+        stats->prefill_seconds = t1 - t0;
+        stats->decode_seconds = t2 - t1;
+    }
+}
+
+} // namespace nut

@@ -1,0 +1,88 @@
+// model.hpp — device-resident model, KV cache and token loop behind the C
+// ABI (the objects nut_model / nut_kvcache point to).
+#pragma once
+
+#include <memory>
+#include <vector>
+
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+struct nut_model;
+struct nut_kvcache;
+
+namespace nut {
+
+struct DeviceLayer {
+    DeviceBuffer storage; // 7 projections + 2 norms, 256-byte aligned
+    LayerView view{};
+    size_t storage_bytes = 0; // reference storage accounting
+    bool set = false;
+};
+
+} // namespace nut
+
+// KVCache on the device (include/kvcache.hpp:8-31): keys and values are
+// [layer][kv_head][position][head_dim] fp32, as src/kvcache.cpp:196-205.
+struct nut_kvcache {
+    nut_config config{};
+    nut::DeviceBuffer keys, values;
+    nut::DeviceBuffer device_length; // int, read by the step kernels
+    size_t length = 0;               // host copy, authoritative
+
+    size_t kv_heads() const
+    {
+        return config.kv_heads == 0 ? config.heads : config.kv_heads;
+    }
+    size_t layer_elements() const
+    {
+        return kv_heads() * config.max_seq * config.head_dim;
+    }
+    void sync_length(hipStream_t stream);
+};
+
+struct nut_model {
+    nut_config config{};
+    int type = 0;
+    bool tied = false;
+    nut::DecodeShape shape{};
+    std::vector<nut::DeviceLayer> layers;
+    nut::DeviceBuffer embeddings, final_norm, lm_head, rope;
+    bool globals_set = false;
+
+    // Step workspace.
+    nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
+    nut::DeviceBuffer part_val, part_idx, state, tokens, prompt;
+    hipStream_t stream = nullptr;
+    std::unique_ptr<nut_kvcache> generation_cache;
+
+    ~nut_model();
+    const float *output_weights() const
+    {
+        return tied ? embeddings.as<float>() : lm_head.as<float>();
+    }
+};
+
+namespace nut {
+
+nut_model *create_model(const nut_config &config, int type, bool tied);
+void set_globals(nut_model &m, const float *embeddings,
+                 const float *final_norm, const float *lm_head);
+void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
+               const float *attention_norm, const float *ffn_norm);
+size_t storage_bytes(const nut_model &m);
+
+nut_kvcache *create_kv(const nut_config &config);
+bool kv_compatible(const nut_kvcache &kv, const nut_config &config);
+
+void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden);
+void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
+             float *hidden);
+void logits(nut_model &m, const float *hidden, float *out);
+void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
+                     size_t max_tokens, int *out, size_t *out_count,
+                     nut_generation_stats *stats);
+
+bool config_valid(const nut_config &c);
+
+} // namespace nut
