@@ -200,6 +200,33 @@ int nut_generate_greedy(nut_model *m, const int *prompt, size_t prompt_len,
                         size_t max_tokens, int *out, size_t *out_count,
                         nut_generation_stats *stats);
 
+/* Execution path of decode / prefill / generate (no reference counterpart;
+ * every path computes the same function): NUT_PATH_AUTO picks the
+ * cooperative token kernel when the shape has an instantiation and the
+ * context fits its fused attention pass, else per-phase step kernels;
+ * NUT_PATH_STEPS forces the step kernels; NUT_PATH_TOKEN forces the token
+ * kernel and fails with NUT_EINVAL where it does not apply. */
+enum { NUT_PATH_AUTO = 0, NUT_PATH_STEPS = 1, NUT_PATH_TOKEN = 2 };
+int nut_model_set_path(nut_model *m, int path);
+
+/* Phase timeline of the cooperative token kernel, for profiling (no
+ * reference counterpart): when enabled, workgroup 0 stamps the device's
+ * constant 100 MHz clock at each phase boundary; per decode iteration
+ * 2 + 9 * layers entries: iteration start, token known, then per layer the
+ * times its QKV input is staged, QKV published, attention input staged,
+ * attention done, Wo published, FFN input staged, gate/up published, down
+ * input staged and down published. nut_model_timeline copies up to
+ * capacity entries of the last launch's timeline. */
+int nut_model_record_timeline(nut_model *m, int enable);
+int nut_model_timeline(const nut_model *m, uint64_t *ticks, size_t capacity,
+                       size_t *count);
+
+/* Device time (HIP events on the model's stream) of the decode loop of the
+ * last nut_generate_greedy call: every classifier, argmax and decode step
+ * after the prefill. (No reference counterpart: GenerationStats carries
+ * host wall time only.) */
+int nut_model_last_decode_ms(const nut_model *m, double *milliseconds);
+
 #ifdef __cplusplus
 }
 #endif

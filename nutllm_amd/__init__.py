@@ -24,6 +24,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libnutllm_hip.so")
 
 INT8, INT4 = 0, 1
+PATH_AUTO, PATH_STEPS, PATH_TOKEN = 0, 1, 2
 
 
 class NutError(Exception):
@@ -119,6 +120,10 @@ _SIGS = {
     "nut_model_set_globals": (C.c_int, [_P, _P, _P, _P]),
     "nut_model_set_layer": (C.c_int, [_P, _SZ] + [_P] * 9),
     "nut_model_storage_bytes": (_SZ, [_P]),
+    "nut_model_last_decode_ms": (C.c_int, [_P, _P]),
+    "nut_model_set_path": (C.c_int, [_P, C.c_int]),
+    "nut_model_record_timeline": (C.c_int, [_P, C.c_int]),
+    "nut_model_timeline": (C.c_int, [_P, _P, _SZ, _P]),
     "nut_model_destroy": (C.c_int, [_P]),
     "nut_kv_create": (C.c_int, [_P, _P]),
     "nut_kv_destroy": (C.c_int, [_P]),
@@ -439,6 +444,30 @@ class DeviceModel:
 
     def storage_bytes(self):
         return lib().nut_model_storage_bytes(self.handle)
+
+    def set_path(self, path):
+        """0 auto, 1 per-phase step kernels, 2 cooperative token kernel."""
+        check(lib().nut_model_set_path(self.handle, path))
+
+    def record_timeline(self, enable=True):
+        check(lib().nut_model_record_timeline(self.handle, int(enable)))
+
+    def timeline(self, iterations):
+        """Phase timeline of the last token-kernel launch, in microseconds
+        from its first mark: array [iterations, 2 + 9 * layers]."""
+        marks = 2 + 9 * self.config.layers
+        out = np.zeros(iterations * marks, np.uint64)
+        n = C.c_size_t()
+        check(lib().nut_model_timeline(self.handle, _ptr(out), out.size,
+                                       C.byref(n)))
+        t = out[:n.value].astype(np.float64).reshape(-1, marks)
+        return (t - t[0, 0]) / 100.0  # 100 MHz ticks -> us
+
+    def last_decode_ms(self):
+        """Device time of the last generate() decode loop (HIP events)."""
+        ms = C.c_double()
+        check(lib().nut_model_last_decode_ms(self.handle, C.byref(ms)))
+        return ms.value
 
     def decode(self, cache, token, want_hidden=True):
         hidden = np.empty(self.config.dim, np.float32) if want_hidden else None

@@ -6,6 +6,8 @@
 
 #include "kernels.hpp"
 #include "model.hpp"
+#include "persistent.hpp"
+#include <algorithm>
 
 namespace nut {
 int select_device(int device);
@@ -250,6 +252,56 @@ int nut_model_set_layer(nut_model *m, size_t layer, const nut_qmatrix *query,
         nut::ensure_device();
         const nut_qmatrix *mats[7] = {query, key, value, output, gate, up, down};
         nut::set_layer(*m, layer, mats, attention_norm, ffn_norm);
+    });
+}
+
+int nut_model_set_path(nut_model *m, int path)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::require(path >= 0 && path <= 2, NUT_EINVAL, "quantized model: unknown path");
+        m->path = path;
+    });
+}
+
+int nut_model_record_timeline(nut_model *m, int enable)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::ensure_device();
+        if (enable) {
+            const size_t n = m->config.max_seq *
+                             size_t(nut::marks_per_iteration(int(m->config.layers)));
+            m->timeline.allocate(n * sizeof(unsigned long long));
+            nut::hip_check(hipMemset(m->timeline.get(), 0, n * sizeof(unsigned long long)),
+                           "hipMemset");
+            m->timeline_entries = n;
+        } else {
+            m->timeline.release();
+            m->timeline_entries = 0;
+        }
+    });
+}
+
+int nut_model_timeline(const nut_model *m, uint64_t *ticks, size_t capacity, size_t *count)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && count != nullptr, NUT_EINVAL, "timeline: null pointer");
+        const size_t n = std::min(capacity, m->timeline_entries);
+        if (n > 0 && ticks != nullptr)
+            nut::hip_check(hipMemcpy(ticks, m->timeline.get(), n * sizeof(uint64_t),
+                                     hipMemcpyDeviceToHost),
+                           "hipMemcpy to host");
+        *count = n;
+    });
+}
+
+int nut_model_last_decode_ms(const nut_model *m, double *milliseconds)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && milliseconds != nullptr, NUT_EINVAL,
+                     "generation: null pointer");
+        *milliseconds = m->last_decode_device_ms;
     });
 }
 

@@ -36,6 +36,58 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// DPP cross-lane moves (GFX9 encodings). Rows are groups of 16 lanes.
+constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v, float fill)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(fill), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp<kDppQuadSwap1>(v, 0.0f);
+    v += dpp<kDppQuadSwap2>(v, 0.0f);
+    v += dpp<kDppRowHalfMirror>(v, 0.0f);
+    v += dpp<kDppRowMirror>(v, 0.0f);
+    return v;
+}
+
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = fmaxf(v, dpp<kDppQuadSwap1>(v, -INFINITY));
+    v = fmaxf(v, dpp<kDppQuadSwap2>(v, -INFINITY));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v, -INFINITY));
+    v = fmaxf(v, dpp<kDppRowMirror>(v, -INFINITY));
+    return v;
+}
+
+// Wave-wide sum / max with DPP (rows, then row broadcasts into lane 63),
+// returned wave-uniform.
+__device__ __forceinline__ float wave_total(float v)
+{
+    v = row16_sum(v);
+    v += dpp<kDppRowBcast15, 0xA>(v, 0.0f);
+    v += dpp<kDppRowBcast31, 0xC>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_maximum(float v)
+{
+    v = row16_max(v);
+    v = fmaxf(v, dpp<kDppRowBcast15, 0xA>(v, -INFINITY));
+    v = fmaxf(v, dpp<kDppRowBcast31, 0xC>(v, -INFINITY));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Sum over a workgroup of `waves` waves; every thread gets the total.
 // `scratch` holds at least `waves` floats of LDS.
 __device__ __forceinline__ float block_sum(float v, float *scratch, int waves)

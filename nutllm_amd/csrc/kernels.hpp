@@ -32,6 +32,40 @@ struct LayerView {
     const float *attention_norm, *ffn_norm;
 };
 
+// Byte layout of one layer in the model's weight arena (every layer
+// identical, pieces 256-byte aligned, block size 32): for query, key,
+// value, output, gate, up, down in turn the packed data then the fp16
+// scales, then the attention and ffn norm vectors. Layer l starts at
+// l * bytes, so a kernel addresses any weight without loading pointers.
+struct LayerLayout {
+    size_t data[7], scales[7], attention_norm, ffn_norm, bytes;
+};
+
+__host__ __device__ constexpr size_t align256(size_t v)
+{
+    return (v + 255) / 256 * 256;
+}
+
+__host__ __device__ constexpr LayerLayout layer_layout(int type, size_t dim,
+                                                       size_t ffn, size_t kvd)
+{
+    LayerLayout l{};
+    const size_t rows[7] = {dim, kvd, kvd, dim, ffn, ffn, dim};
+    const size_t cols[7] = {dim, dim, dim, dim, dim, dim, ffn};
+    size_t total = 0;
+    for (int i = 0; i < 7; i++) {
+        const size_t n = rows[i] * cols[i];
+        l.data[i] = total;
+        total = align256(total + (type == 1 ? (n + 1) / 2 : n));
+        l.scales[i] = total;
+        total = align256(total + 2 * ((n + 31) / 32));
+    }
+    l.attention_norm = total;
+    l.ffn_norm = total + dim * 4;
+    l.bytes = align256(total + 2 * dim * 4);
+    return l;
+}
+
 struct DecodeShape {
     int dim, heads, kv_heads, head_dim, ffn_dim, vocab, max_seq, eos;
     float attn_scale;

@@ -3,6 +3,7 @@
 // generation). Validation and messages follow the reference's exceptions
 // (src/quant_model.cpp:161-172,212-213; src/generate.cpp:177-181).
 #include "model.hpp"
+#include "persistent.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -144,6 +145,8 @@ nut_model *create_model(const nut_config &config, int type, bool tied)
     m->prompt.allocate((config.max_seq + 1) * sizeof(int));
     hip_check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking),
               "hipStreamCreate");
+    hip_check(hipEventCreate(&m->decode_begin), "hipEventCreate");
+    hip_check(hipEventCreate(&m->decode_end), "hipEventCreate");
     return m.release();
 }
 
@@ -261,11 +264,102 @@ void nut_kvcache::sync_length(hipStream_t stream)
 
 nut_model::~nut_model()
 {
+    if (decode_begin != nullptr)
+        (void)hipEventDestroy(decode_begin);
+    if (decode_end != nullptr)
+        (void)hipEventDestroy(decode_end);
     if (stream != nullptr)
         (void)hipStreamDestroy(stream);
 }
 
 namespace nut {
+
+namespace {
+
+// The cooperative token kernel runs when the model shape has an
+// instantiation, the device can hold its grid, and every position of the
+// launch fits the fused attention pass.
+bool use_token_kernel(nut_model &m, size_t end_length)
+{
+    if (m.path == 1)
+        return false;
+    const bool ok = token_kernel_supported(m.type, m.shape) &&
+                    end_length <= size_t(token_kernel_max_positions(m.type, m.shape));
+    if (m.path == 2 && !ok)
+        fail(NUT_EINVAL, "token kernel: shape or context not supported");
+    return ok;
+}
+
+void prepare_token_kernel(nut_model &m)
+{
+    if (m.layer_views.get() == nullptr) {
+        std::vector<LayerView> views;
+        for (const DeviceLayer &l : m.layers)
+            views.push_back(l.view);
+        m.layer_views.allocate(views.size() * sizeof(LayerView));
+        upload(m.layer_views.get(), views.data(), views.size() * sizeof(LayerView));
+        const size_t entries = token_exchange_entries(m.shape);
+        m.exchange.allocate(entries * sizeof(uint64_t));
+        hip_check(hipMemset(m.exchange.get(), 0, entries * sizeof(uint64_t)), "hipMemset");
+        m.token_error.allocate(sizeof(int));
+    }
+}
+
+// Enqueue one launch; iteration it decodes position start + it.
+void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter,
+                      bool classify, const int *tokens_in, const float *hidden_in,
+                      float *hidden_out)
+{
+    prepare_token_kernel(m);
+    const DecodeShape &s = m.shape;
+    const size_t kvd = size_t(s.kv_heads) * s.head_dim;
+    uint64_t *x = m.exchange.as<uint64_t>();
+    TokenArgs a{};
+    a.layers = m.layer_views.as<LayerView>();
+    a.embeddings = m.embeddings.as<float>();
+    a.final_norm = m.final_norm.as<float>();
+    a.classifier = m.output_weights();
+    a.rope = m.rope.as<float2>();
+    a.k_cache = kv.keys.as<float>();
+    a.v_cache = kv.values.as<float>();
+    a.x_qkv = x;
+    a.x_hidden = x + s.dim + 2 * kvd;
+    a.x_act = a.x_hidden + s.dim;
+    a.x_part = a.x_act + s.ffn_dim;
+    a.hidden_in = hidden_in;
+    a.hidden_out = hidden_out;
+    a.tokens_in = tokens_in;
+    a.tokens_out = m.tokens.as<int>();
+    a.state = m.state.as<StepState>();
+    a.error = m.token_error.as<int>();
+    a.tag_base = (++m.launch_count) << 20;
+    a.layer_count = int(m.config.layers);
+    a.vocab = s.vocab;
+    a.max_seq = s.max_seq;
+    a.eos = s.eos;
+    a.start_len = int(start);
+    a.n_iter = int(n_iter);
+    a.classify = classify ? 1 : 0;
+    a.attn_scale = s.attn_scale;
+    a.timeline = m.timeline_entries > 0 ? m.timeline.as<unsigned long long>() : nullptr;
+    a.timeline_cap = int(m.timeline_entries);
+    launch_set_int(a.error, 0, m.stream);
+    launch_token_kernel(m.type, s, a, m.stream);
+}
+
+// After the stream synchronised: raise the kernel's bounded-wait failure.
+void check_token_error(nut_model &m)
+{
+    if (m.token_error.get() == nullptr)
+        return;
+    int error = 0;
+    hip_check(hipMemcpy(&error, m.token_error.get(), sizeof error, hipMemcpyDeviceToHost),
+              "hipMemcpy");
+    if (error != 0)
+        fail(NUT_EDEVICE, "token kernel: phase exchange timed out");
+}
+
+} // namespace
 
 void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden)
 {
@@ -277,14 +371,21 @@ void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden)
             "quantized decode: token out of range");
     require(kv.length < kv.config.max_seq, NUT_ELENGTH,
             "quantized decode: context is full");
-    kv.sync_length(m.stream);
-    launch_reset_state(m.state.as<StepState>(), token, m.stream);
-    enqueue_step(m, kv, &m.state.as<StepState>()->token);
+    if (use_token_kernel(m, kv.length + 1)) {
+        launch_set_int(m.prompt.as<int>(), token, m.stream);
+        run_token_kernel(m, kv, kv.length, 1, false, m.prompt.as<int>(), nullptr,
+                         m.hidden.as<float>());
+    } else {
+        kv.sync_length(m.stream);
+        launch_reset_state(m.state.as<StepState>(), token, m.stream);
+        enqueue_step(m, kv, &m.state.as<StepState>()->token);
+    }
     if (hidden != nullptr)
         hip_check(hipMemcpyAsync(hidden, m.hidden.get(), m.config.dim * sizeof(float),
                                  hipMemcpyDeviceToHost, m.stream),
                   "hipMemcpyAsync");
     sync(m);
+    check_token_error(m);
     kv.length += 1;
 }
 
@@ -308,15 +409,21 @@ void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
         hip_check(hipMemcpyAsync(m.prompt.get(), tokens, valid * sizeof(int),
                                  hipMemcpyHostToDevice, m.stream),
                   "hipMemcpyAsync");
-        kv.sync_length(m.stream);
-        launch_reset_state(m.state.as<StepState>(), tokens[0], m.stream);
-        for (size_t t = 0; t < valid; t++)
-            enqueue_step(m, kv, m.prompt.as<int>() + t);
+        if (use_token_kernel(m, valid)) {
+            run_token_kernel(m, kv, 0, valid, false, m.prompt.as<int>(), nullptr,
+                             m.hidden.as<float>());
+        } else {
+            kv.sync_length(m.stream);
+            launch_reset_state(m.state.as<StepState>(), tokens[0], m.stream);
+            for (size_t t = 0; t < valid; t++)
+                enqueue_step(m, kv, m.prompt.as<int>() + t);
+        }
         if (hidden != nullptr)
             hip_check(hipMemcpyAsync(hidden, m.hidden.get(), m.config.dim * sizeof(float),
                                      hipMemcpyDeviceToHost, m.stream),
                       "hipMemcpyAsync");
         sync(m);
+        check_token_error(m);
         kv.length = valid;
     }
     require(valid == count, NUT_EOUTOFRANGE, "quantized decode: token out of range");
@@ -361,20 +468,33 @@ void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
     StepState *state = m.state.as<StepState>();
     launch_reset_state(state, 0, m.stream);
     const int parts = classifier_blocks(m.shape);
-    for (size_t i = 0; i < steps; i++) {
-        launch_classifier(m.shape, m.hidden.as<float>(), m.final_norm.as<float>(),
-                          m.output_weights(), nullptr, m.part_val.as<float>(),
-                          m.part_idx.as<int>(), state, m.stream);
-        launch_pick_token(m.shape, m.part_val.as<float>(), m.part_idx.as<int>(),
-                          parts, state, m.tokens.as<int>(), m.stream);
-        enqueue_step(m, kv, &state->token);
+    const bool fused = steps > 0 && use_token_kernel(m, prompt_len + steps);
+    hip_check(hipEventRecord(m.decode_begin, m.stream), "hipEventRecord");
+    if (fused) {
+        run_token_kernel(m, kv, prompt_len, steps, true, nullptr, m.hidden.as<float>(),
+                         m.scratch_hidden.as<float>());
+    } else {
+        for (size_t i = 0; i < steps; i++) {
+            launch_classifier(m.shape, m.hidden.as<float>(), m.final_norm.as<float>(),
+                              m.output_weights(), nullptr, m.part_val.as<float>(),
+                              m.part_idx.as<int>(), state, m.stream);
+            launch_pick_token(m.shape, m.part_val.as<float>(), m.part_idx.as<int>(),
+                              parts, state, m.tokens.as<int>(), m.stream);
+            enqueue_step(m, kv, &state->token);
+        }
     }
+    hip_check(hipEventRecord(m.decode_end, m.stream), "hipEventRecord");
     StepState host_state{};
     hip_check(hipMemcpyAsync(&host_state, state, sizeof host_state,
                              hipMemcpyDeviceToHost, m.stream),
               "hipMemcpyAsync");
     sync(m);
     const double t2 = now();
+    check_token_error(m);
+    float device_ms = 0.0f;
+    hip_check(hipEventElapsedTime(&device_ms, m.decode_begin, m.decode_end),
+              "hipEventElapsedTime");
+    m.last_decode_device_ms = device_ms;
     const size_t count = size_t(host_state.count);
     if (count > 0)
         hip_check(hipMemcpy(out, m.tokens.get(), count * sizeof(int),

@@ -54,6 +54,13 @@ struct nut_model {
     nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
     nut::DeviceBuffer part_val, part_idx, state, tokens, prompt;
     hipStream_t stream = nullptr;
+    hipEvent_t decode_begin = nullptr, decode_end = nullptr;
+    // Cooperative token kernel state.
+    int path = 0; // 0 auto, 1 step kernels, 2 token kernel
+    nut::DeviceBuffer layer_views, exchange, token_error, timeline;
+    size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
+    unsigned launch_count = 0;
+    double last_decode_device_ms = 0.0; // events around the decode loop
     std::unique_ptr<nut_kvcache> generation_cache;
 
     ~nut_model();

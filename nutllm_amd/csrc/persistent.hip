@@ -1,0 +1,971 @@
+// persistent.hip — the quantised token loop as one cooperative kernel.
+//
+// One workgroup per CU (256 x 512 threads) runs every phase of every token:
+//   A  rmsnorm(h) -> Q/K/V rows, RoPE, K/V cache store
+//   B  GQA attention over positions 0..pos for all heads, then Wo rows and
+//      the residual add
+//   C  rmsnorm(h) -> gate/up rows, silu(gate) * up
+//   D  W2 rows and the residual add
+// and, when generating, the final rmsnorm + fp32 classifier + first-index
+// argmax (src/generate.cpp:195-207) before each decode step.
+//
+// Phases exchange activations through HBM as 64-bit (value, tag) words
+// written with agent-scope (sc1) stores; a consumer polls the words it needs
+// until they carry the producing phase's tag, so the flag is the data itself
+// and no cache-wide writeback or invalidate is needed.
+//
+// Latency hiding: before a workgroup waits for a phase's input, it starts
+// LDS DMA (global_load_lds_dwordx4) of that phase's weight rows — and, for
+// attention, of the K/V rows of earlier positions — so HBM streams during
+// the wait and nothing is held in registers across it.
+//
+// Every wait is bounded: on timeout the kernel raises an error flag that all
+// waits observe, and every workgroup runs to the end.
+#include "persistent.hpp"
+#include "runtime.hpp"
+
+namespace nut {
+
+namespace {
+
+constexpr int kGrid = 256;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kSpinLimit = 200000;
+
+constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <int QT_, int DIM_, int FFN_, int HEADS_, int KVH_, int HD_, int NP_>
+struct Geo {
+    static constexpr int QT = QT_, DIM = DIM_, FFN = FFN_, HEADS = HEADS_;
+    static constexpr int KVH = KVH_, HD = HD_;
+    static constexpr int NP = NP_; // positions of the fused attention
+    static constexpr int KVD = KVH * HD, GROUP = HEADS / KVH;
+    static constexpr int HPW = HEADS / kWaves; // attention heads per wave
+    static constexpr int BLK_DIM = DIM / 32, BLK_FFN = FFN / 32;
+    static constexpr int CPL_DIM = cdiv(BLK_DIM, kWave); // blocks per lane
+    static constexpr int CPL_FFN = cdiv(BLK_FFN, kWave);
+    // bytes of one quantised row (data, fp16 scales) for input dim / ffn
+    static constexpr int RB_DIM = QT == 1 ? DIM / 2 : DIM;
+    static constexpr int RB_FFN = QT == 1 ? FFN / 2 : FFN;
+    static constexpr int SB_DIM = 2 * BLK_DIM, SB_FFN = 2 * BLK_FFN;
+    // rows one workgroup owns in each phase (upper bounds)
+    static constexpr int ROWS_QKV = 2 * cdiv((DIM + 2 * KVD) / 2, kGrid);
+    static constexpr int ROWS_WO = cdiv(DIM, kGrid);
+    static constexpr int ROWS_GU = 2 * cdiv(FFN, kGrid);
+    static constexpr int ROWS_DN = cdiv(DIM, kGrid);
+    // LDS staging: region 1 holds, in turn, K/V rows and the QKV, gate/up
+    // and down weight rows; region 2 the Wo rows (live across attention)
+    static constexpr int KV_BYTES = 2 * KVH * NP * HD * 4;
+    static constexpr int W_QKV = ROWS_QKV * (RB_DIM + SB_DIM);
+    static constexpr int W_GU = ROWS_GU * (RB_DIM + SB_DIM);
+    static constexpr int W_DN = ROWS_DN * (RB_FFN + SB_FFN);
+    static constexpr int W_WO = ROWS_WO * (RB_DIM + SB_DIM);
+    static constexpr int R1 = cmax(cmax(KV_BYTES, W_QKV), cmax(W_GU, W_DN));
+    static constexpr int R2 = W_WO;
+    static_assert(DIM % 32 == 0 && FFN % 32 == 0, "block-aligned rows");
+    static_assert(RB_FFN % 16 == 0 && SB_FFN % 16 == 0 && SB_DIM % 16 == 0,
+                  "16-byte DMA granules");
+    static_assert(HEADS % kWaves == 0, "heads split over waves");
+    static_assert(HD % 4 == 0 && kWave % (HD / 4) == 0, "head_dim");
+    static_assert((DIM + 2 * KVD) % 2 == 0 && KVD % 2 == 0, "row pairs");
+};
+
+// ------------------------------------------------------------ exchange --
+
+__device__ __forceinline__ uint64_t load_coherent(const uint64_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void store_coherent(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void put(uint64_t *p, float v, unsigned tag)
+{
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool failed(const int *error)
+{
+    return __hip_atomic_load(error, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// The error flag as seen by thread 0, made uniform over the workgroup so
+// every thread takes the same branch.
+__device__ __forceinline__ bool wg_failed(const int *error, int *slot)
+{
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *slot = failed(error) ? 1 : 0;
+    __syncthreads();
+    return *slot != 0;
+}
+
+// Re-poll *p until its tag matches (bounded; gives up once any wait failed).
+__device__ __noinline__ uint64_t wait_tag(const uint64_t *p, unsigned tag,
+                                          int *error)
+{
+    uint64_t v = load_coherent(p);
+    int spins = 0;
+    while (unsigned(v >> 32) != tag) {
+        __builtin_amdgcn_s_sleep(2);
+        v = load_coherent(p);
+        if ((++spins & 63) == 0 && failed(error))
+            break;
+        if (spins > kSpinLimit) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    return v;
+}
+
+__device__ __forceinline__ int wave_index()
+{
+    return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
+
+// --------------------------------------------------------------- LDS DMA --
+
+// Copy `bytes` (a multiple of 16) from global memory to LDS without
+// registers: 1 KB per wave instruction, lane i moving bytes [16i, 16i+16) of
+// its kilobyte; instructions are spread over the workgroup's waves.
+// Completion: s_waitcnt vmcnt(0) in every wave, then a workgroup barrier.
+__device__ __forceinline__ void dma(void *lds_dst, const void *src, int bytes)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = (bytes + 1023) >> 10;
+    for (int i = wave_index(); i < n; i += kWaves) {
+        const int off = (i << 10) + (lane << 4);
+        if (off < bytes)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(
+                    static_cast<const char *>(src) + off),
+                (__attribute__((address_space(3))) void *)(
+                    static_cast<char *>(lds_dst) + (i << 10)),
+                16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void dma_wait()
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+
+// --------------------------------------------------------- x staging --
+
+// Element i of x lives at swz(i): quads of each 32-element block are
+// rotated by the block index, so lane b reading quad q of block b hits a
+// different 16-byte bank group than lanes b+1..b+7.
+__device__ __forceinline__ int swz(int i)
+{
+    const int b = i >> 5, q = (i >> 2) & 7;
+    return (b << 5) | (((q + b) & 7) << 2) | (i & 3);
+}
+
+__device__ __forceinline__ void load_x_block(const float *xs, int b,
+                                             float4 (&xq)[8])
+{
+    const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+        xq[q] = base[(q + b) & 7];
+}
+
+// Workgroup sum of per-thread values; every thread gets the total.
+__device__ __forceinline__ float wg_sum(float v, float *red)
+{
+    v = wave_total(v);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    __syncthreads();
+    if (lane == 0)
+        red[wave] = v;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++)
+        total += red[w];
+    return total;
+}
+
+__device__ void block_sums(const float *xs, float *xsum, int n)
+{
+    for (int b = threadIdx.x; b < n / 32; b += kThreads) {
+        const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            s += (base[q].x + base[q].y) + (base[q].z + base[q].w);
+        xsum[b] = s;
+    }
+    __syncthreads();
+}
+
+// xs (swizzled) = src * scale * w, plus block sums; ends with a barrier.
+__device__ void stage_x(const float *src, const float *weight, float scale,
+                        float *xs, float *xsum, int n)
+{
+    for (int i = threadIdx.x; i < n; i += kThreads)
+        xs[swz(i)] = src[i] * scale * weight[i];
+    __syncthreads();
+    block_sums(xs, xsum, n);
+}
+
+__device__ __forceinline__ float rms_scale(float squares, int n)
+{
+    return 1.0f / sqrtf(squares / float(n) + 1e-5f);
+}
+
+// dst[map(i)] = value of src[i] once tagged, i < N (all loads issued before
+// the first tag test: one coherent round trip); returns this thread's sum of
+// squares. Waits for this wave's outstanding DMA, then a barrier.
+template <int N, bool SWIZZLE>
+__device__ float take(const uint64_t *src, float *dst, unsigned tag,
+                      int *error)
+{
+    constexpr int PER = cdiv(N, kThreads);
+    uint64_t v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        v[u] = i < N ? load_coherent(src + i) : 0;
+    }
+    float squares = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < N) {
+            if (unsigned(v[u] >> 32) != tag)
+                v[u] = wait_tag(src + i, tag, error);
+            const float f = __uint_as_float(unsigned(v[u]));
+            dst[SWIZZLE ? swz(i) : i] = f;
+            squares = fmaf(f, f, squares);
+        }
+    }
+    dma_wait();
+    return squares;
+}
+
+// ------------------------------------------------------ quantised rows --
+
+__device__ __forceinline__ float dot_block_int4(const uint4 &w,
+                                                const float4 (&x)[8])
+{
+    const uint32_t words[4] = {w.x ^ 0x88888888u, w.y ^ 0x88888888u,
+                               w.z ^ 0x88888888u, w.w ^ 0x88888888u};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t lo = words[j] & 0x0f0f0f0fu;
+        const uint32_t hi = (words[j] >> 4) & 0x0f0f0f0fu;
+        const float4 xa = x[2 * j], xb = x[2 * j + 1];
+        a0 = fmaf(ubyte0(lo), xa.x, a0);
+        a1 = fmaf(ubyte0(hi), xa.y, a1);
+        a0 = fmaf(ubyte1(lo), xa.z, a0);
+        a1 = fmaf(ubyte1(hi), xa.w, a1);
+        a0 = fmaf(ubyte2(lo), xb.x, a0);
+        a1 = fmaf(ubyte2(hi), xb.y, a1);
+        a0 = fmaf(ubyte3(lo), xb.z, a0);
+        a1 = fmaf(ubyte3(hi), xb.w, a1);
+    }
+    return a0 + a1;
+}
+
+__device__ __forceinline__ float dot_block_int8(const uint4 &w0,
+                                                const uint4 &w1,
+                                                const float4 (&x)[8])
+{
+    const uint32_t words[8] = {w0.x ^ 0x80808080u, w0.y ^ 0x80808080u,
+                               w0.z ^ 0x80808080u, w0.w ^ 0x80808080u,
+                               w1.x ^ 0x80808080u, w1.y ^ 0x80808080u,
+                               w1.z ^ 0x80808080u, w1.w ^ 0x80808080u};
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        a0 = fmaf(ubyte0(words[j]), x[j].x, a0);
+        a1 = fmaf(ubyte1(words[j]), x[j].y, a1);
+        a0 = fmaf(ubyte2(words[j]), x[j].z, a0);
+        a1 = fmaf(ubyte3(words[j]), x[j].w, a1);
+    }
+    return a0 + a1;
+}
+
+// Block b of a staged row (data in LDS) dotted with x quads, minus the
+// offset-binary bias, times the block's fp16 scale.
+template <int QT>
+__device__ __forceinline__ float block_term(const uint8_t *row,
+                                           const uint16_t *scales, int b,
+                                           const float4 (&xq)[8], float xsum)
+{
+    float d;
+    if (QT == 1) {
+        d = dot_block_int4(reinterpret_cast<const uint4 *>(row)[b], xq) -
+            8.0f * xsum;
+    } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
+        d = dot_block_int8(p[0], p[1], xq) - 128.0f * xsum;
+    }
+    return half_bits_to_float(scales[b]) * d;
+}
+
+// x of one phase held in registers, lane's blocks b = lane + 64 j.
+template <int CPL> struct XRegs {
+    float4 q[CPL][8];
+    float sum[CPL];
+};
+
+template <int CPL>
+__device__ __forceinline__ void load_x(XRegs<CPL> &x, const float *xs,
+                                       const float *xsum, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks) {
+            load_x_block(xs, b, x.q[j]);
+            x.sum[j] = xsum[b];
+        }
+    }
+}
+
+// Wave dot product of a staged row with x in registers; all lanes get it.
+template <int QT, int CPL>
+__device__ __forceinline__ float row_dot(const uint8_t *row,
+                                         const uint16_t *scales,
+                                         const XRegs<CPL> &x, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks)
+            acc += block_term<QT>(row, scales, b, x.q[j], x.sum[j]);
+    }
+    return wave_total(acc);
+}
+
+// As row_dot, reading x from LDS (rows swept once per wave).
+template <int QT, int CPL>
+__device__ __forceinline__ float row_dot_lds(const uint8_t *row,
+                                             const uint16_t *scales,
+                                             const float *xs,
+                                             const float *xsum, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks) {
+            float4 xq[8];
+            load_x_block(xs, b, xq);
+            acc += block_term<QT>(row, scales, b, xq, xsum[b]);
+        }
+    }
+    return wave_total(acc);
+}
+
+__device__ __forceinline__ const uint8_t *row_data(const QMat &m, int row)
+{
+    return m.data + size_t(row) * (m.type == 1 ? m.cols / 2 : m.cols);
+}
+
+__device__ __forceinline__ const uint16_t *row_scales(const QMat &m, int row)
+{
+    return m.scales + size_t(row) * (m.cols / 32);
+}
+
+// Units [begin, end) of `units` owned by this workgroup.
+__device__ __forceinline__ void wg_share(int units, int &begin, int &end)
+{
+    begin = int((long long)units * blockIdx.x / kGrid);
+    end = int((long long)units * (blockIdx.x + 1) / kGrid);
+}
+
+// DMA rows [lo, hi) of m into LDS row slots starting at slot `first`.
+template <int RB, int SB, int ROWS>
+__device__ __forceinline__ void stage_rows(uint8_t *region, const QMat &m,
+                                           int lo, int hi, int first)
+{
+    if (hi <= lo)
+        return;
+    dma(region + first * RB, row_data(m, lo), (hi - lo) * RB);
+    dma(region + ROWS * RB + first * SB, row_scales(m, lo), (hi - lo) * SB);
+}
+
+// ------------------------------------------------------------- kernel --
+
+template <class G> struct Lds {
+    static constexpr int XN = cmax(G::FFN, G::DIM);
+    static constexpr int H = 0;                      // raw h [DIM]
+    static constexpr int X = H + G::DIM;             // swizzled x
+    static constexpr int XSUM = X + XN;              // block sums
+    static constexpr int QKV = XSUM + XN / 32;       // q, k, v staging
+    static constexpr int SCORES = QKV + G::DIM + 2 * G::KVD;
+    static constexpr int R1 = cdiv(SCORES + kWaves * G::HPW * G::NP, 4) * 4;
+    static constexpr int R2 = R1 + G::R1 / 4;
+    static constexpr int RED = R2 + G::R2 / 4;
+    static constexpr int MISC = RED + 2 * kWaves; // 16 ints
+    static constexpr int TOTAL = MISC + 16;
+    static constexpr size_t BYTES = size_t(TOTAL) * sizeof(float);
+    static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+template <class G>
+__global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
+{
+    extern __shared__ float4 lds4[];
+    float *lds = reinterpret_cast<float *>(lds4);
+    using L = Lds<G>;
+    float *h_raw = lds + L::H, *xs = lds + L::X, *xsum = lds + L::XSUM;
+    float *qkv = lds + L::QKV, *scores = lds + L::SCORES, *red = lds + L::RED;
+    uint8_t *r1 = reinterpret_cast<uint8_t *>(lds + L::R1);
+    uint8_t *r2 = reinterpret_cast<uint8_t *>(lds + L::R2);
+    float *kst = lds + L::R1;                       // [KVH][NP][HD]
+    float *vst = kst + G::KVH * G::NP * G::HD;
+    int *misc = reinterpret_cast<int *>(lds + L::MISC);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = wave_index();
+    unsigned tag = a.tag_base;
+    int *error = a.error;
+    const size_t kv_layer = size_t(G::KVH) * a.max_seq * G::HD;
+    const int marks = marks_per_iteration(a.layer_count);
+    // Phase timeline: workgroup 0 stamps entry k of iteration `it`.
+    auto mark = [&](int it, int k) {
+        if (a.timeline != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+            const int i = it * marks + k;
+            if (i < a.timeline_cap)
+                a.timeline[i] = __builtin_amdgcn_s_memrealtime();
+        }
+    };
+
+    int qkv_b, qkv_e, wo_b, wo_e, gu_b, gu_e, dn_b, dn_e;
+    wg_share((G::DIM + 2 * G::KVD) / 2, qkv_b, qkv_e); // row pairs
+    wg_share(G::DIM, wo_b, wo_e);
+    wg_share(G::FFN, gu_b, gu_e); // (gate, up) pairs
+    wg_share(G::DIM, dn_b, dn_e);
+
+    // Weight staging of each phase (region and slot layout).
+    auto stage_qkv = [&](int layer) {
+        const LayerView &w = a.layers[layer];
+        const int lo = 2 * qkv_b, hi = 2 * qkv_e;
+        const int q_hi = G::DIM, k_hi = G::DIM + G::KVD;
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
+            r1, w.query, lo, min(hi, q_hi), 0);
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
+            r1, w.key, max(lo, q_hi) - q_hi, min(hi, k_hi) - q_hi,
+            max(lo, q_hi) - lo);
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
+            r1, w.value, max(lo, k_hi) - k_hi, hi - k_hi, max(lo, k_hi) - lo);
+    };
+    auto stage_wo = [&](int layer) {
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_WO>(r2, a.layers[layer].output,
+                                                     wo_b, wo_e, 0);
+    };
+    auto stage_gu = [&](int layer) {
+        const LayerView &w = a.layers[layer];
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_GU>(r1, w.gate, gu_b, gu_e, 0);
+        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_GU>(r1, w.up, gu_b, gu_e,
+                                                     G::ROWS_GU / 2);
+    };
+    auto stage_down = [&](int layer) {
+        stage_rows<G::RB_FFN, G::SB_FFN, G::ROWS_DN>(r1, a.layers[layer].down,
+                                                     dn_b, dn_e, 0);
+    };
+    auto slot = [&](int rows, int rb, int sb, int s, const uint8_t *&d,
+                    const uint16_t *&sc, const uint8_t *region) {
+        d = region + s * rb;
+        sc = reinterpret_cast<const uint16_t *>(region + rows * rb + s * sb);
+    };
+
+    int count = 0, done = 0, last_token = 0;
+    // Tag of the hidden state the next classifier reads; 0 = hidden_in.
+    unsigned hidden_tag = 0;
+
+    for (int it = 0; it < a.n_iter && !done; it++) {
+        int token;
+        mark(it, 0);
+        if (a.classify) {
+            // ---------------- final rmsnorm + classifier + argmax ----
+            const float *wcls = a.classifier;
+            float sq;
+            if (hidden_tag == 0) {
+                sq = 0.0f;
+                for (int i = threadIdx.x; i < G::DIM; i += kThreads) {
+                    const float v = a.hidden_in[i];
+                    h_raw[i] = v;
+                    sq = fmaf(v, v, sq);
+                }
+                __syncthreads();
+            } else {
+                sq = take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
+            }
+            const float scale = rms_scale(wg_sum(sq, red), G::DIM);
+            // plain layout: lane needs x[4c..4c+3], c = lane + 64 j
+            for (int i = threadIdx.x; i < G::DIM; i += kThreads)
+                xs[i] = h_raw[i] * scale * a.final_norm[i];
+            __syncthreads();
+            constexpr int C4 = G::DIM / 4 / kWave; // float4 per lane per row
+            const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+            int rb, re;
+            {
+                int wb, we;
+                wg_share(a.vocab, wb, we);
+                rb = wb + (we - wb) * wave / kWaves;
+                re = wb + (we - wb) * (wave + 1) / kWaves;
+            }
+            float best_v = -INFINITY;
+            int best_i = 0x7fffffff;
+            for (int row = rb; row < re; row += 2) {
+                const bool two = row + 1 < re;
+                const float4 *w0 = reinterpret_cast<const float4 *>(wcls + size_t(row) * G::DIM);
+                const float4 *w1 = reinterpret_cast<const float4 *>(wcls + size_t(two ? row + 1 : row) * G::DIM);
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int j0 = 0; j0 < C4; j0 += 4) {
+                    float4 v0[4], v1[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        v0[j] = w0[lane + kWave * (j0 + j)];
+                        v1[j] = w1[lane + kWave * (j0 + j)];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float4 x = x4[lane + kWave * (j0 + j)];
+                        s0 = fmaf(v0[j].x, x.x, s0);
+                        s0 = fmaf(v0[j].y, x.y, s0);
+                        s0 = fmaf(v0[j].z, x.z, s0);
+                        s0 = fmaf(v0[j].w, x.w, s0);
+                        s1 = fmaf(v1[j].x, x.x, s1);
+                        s1 = fmaf(v1[j].y, x.y, s1);
+                        s1 = fmaf(v1[j].z, x.z, s1);
+                        s1 = fmaf(v1[j].w, x.w, s1);
+                    }
+                }
+                s0 = wave_total(s0);
+                s1 = wave_total(s1);
+                if (s0 > best_v) {
+                    best_v = s0;
+                    best_i = row;
+                }
+                if (two && s1 > best_v) {
+                    best_v = s1;
+                    best_i = row + 1;
+                }
+            }
+            __syncthreads();
+            // Layer 0's QKV rows stream into LDS during the argmax exchange.
+            stage_qkv(0);
+            if (lane == 0) {
+                red[wave] = best_v;
+                misc[wave] = best_i;
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                float bv = red[0];
+                int bi = misc[0];
+                for (int w = 1; w < kWaves; w++)
+                    if (red[w] > bv || (red[w] == bv && misc[w] < bi)) {
+                        bv = red[w];
+                        bi = misc[w];
+                    }
+                // the block's best (value, index) as two tagged words
+                put(a.x_part + blockIdx.x, bv, tag);
+                put(a.x_part + kGrid + blockIdx.x, __int_as_float(bi), tag);
+            }
+            // every workgroup reduces all partials to the same token
+            float pv = -INFINITY;
+            int pi = 0x7fffffff;
+            if (threadIdx.x < kGrid) {
+                uint64_t v = load_coherent(a.x_part + threadIdx.x);
+                uint64_t i = load_coherent(a.x_part + kGrid + threadIdx.x);
+                if (unsigned(v >> 32) != tag)
+                    v = wait_tag(a.x_part + threadIdx.x, tag, error);
+                if (unsigned(i >> 32) != tag)
+                    i = wait_tag(a.x_part + kGrid + threadIdx.x, tag, error);
+                pv = __uint_as_float(unsigned(v));
+                pi = int(unsigned(i));
+            }
+            tag++;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(pv, off);
+                const int oi = __shfl_xor(pi, off);
+                if (ov > pv || (ov == pv && oi < pi)) {
+                    pv = ov;
+                    pi = oi;
+                }
+            }
+            __syncthreads();
+            if (lane == 0) {
+                red[wave] = pv;
+                misc[wave] = pi;
+            }
+            __syncthreads();
+            float bv = red[0];
+            int bi = misc[0];
+            for (int w = 1; w < kWaves; w++)
+                if (red[w] > bv || (red[w] == bv && misc[w] < bi)) {
+                    bv = red[w];
+                    bi = misc[w];
+                }
+            token = (bi >= 0 && bi < a.vocab) ? bi : 0;
+            if (wg_failed(error, misc + 8))
+                break;
+            if (token == a.eos) {
+                done = 1;
+                break;
+            }
+            if (blockIdx.x == 0 && threadIdx.x == 0)
+                a.tokens_out[count] = token;
+            count++;
+        } else {
+            token = a.tokens_in[it];
+            stage_qkv(0);
+        }
+        last_token = token;
+        const int pos = a.start_len + it;
+        mark(it, 1);
+
+        for (int l = 0; l < a.layer_count; l++) {
+            const LayerView &w = a.layers[l];
+            float *kc = a.k_cache + l * kv_layer;
+            float *vc = a.v_cache + l * kv_layer;
+
+            // ---------------------------------------------- phase A: qkv --
+            // RoPE factors of this wave's first pair, read before the wait.
+            float2 rope_cs = make_float2(1.0f, 0.0f);
+            if (wave < qkv_e - qkv_b) {
+                const int row = 2 * (qkv_b + wave);
+                const int local = row < G::DIM ? row : row - G::DIM;
+                if (row < G::DIM + G::KVD)
+                    rope_cs = a.rope[size_t(pos) * (G::HD / 2) + (local % G::HD) / 2];
+            }
+            float sq;
+            if (l == 0) {
+                sq = 0.0f;
+                const float *e = a.embeddings + size_t(token) * G::DIM;
+                for (int i = threadIdx.x; i < G::DIM; i += kThreads) {
+                    const float v = e[i];
+                    h_raw[i] = v;
+                    sq = fmaf(v, v, sq);
+                }
+                dma_wait();
+            } else {
+                sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
+            }
+            stage_x(h_raw, w.attention_norm, rms_scale(wg_sum(sq, red), G::DIM),
+                    xs, xsum, G::DIM);
+            mark(it, 2 + 9 * l);
+            {
+                XRegs<G::CPL_DIM> x;
+                load_x(x, xs, xsum, G::BLK_DIM);
+                for (int pair = wave; pair < qkv_e - qkv_b; pair += kWaves) {
+                    const int row = 2 * (qkv_b + pair);
+                    const uint8_t *d0, *d1;
+                    const uint16_t *s0, *s1;
+                    slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, 2 * pair, d0, s0, r1);
+                    slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, 2 * pair + 1, d1, s1, r1);
+                    float e0 = row_dot<G::QT>(d0, s0, x, G::BLK_DIM);
+                    float e1 = row_dot<G::QT>(d1, s1, x, G::BLK_DIM);
+                    if (lane == 0) {
+                        const int which = row < G::DIM ? 0 : row < G::DIM + G::KVD ? 1 : 2;
+                        const int local = which == 0 ? row : which == 1 ? row - G::DIM
+                                                                        : row - G::DIM - G::KVD;
+                        const int head = local / G::HD, d = local % G::HD;
+                        if (which < 2) {
+                            const float2 cs = pair == wave ? rope_cs
+                                : a.rope[size_t(pos) * (G::HD / 2) + d / 2];
+                            const float even = e0, odd = e1;
+                            e0 = fmaf(even, cs.x, -(odd * cs.y));
+                            e1 = fmaf(even, cs.y, odd * cs.x);
+                        }
+                        put(a.x_qkv + row, e0, tag);
+                        put(a.x_qkv + row + 1, e1, tag);
+                        if (which > 0) {
+                            float *cache = (which == 1 ? kc : vc) +
+                                           (size_t(head) * a.max_seq + pos) * G::HD + d;
+                            store_coherent(cache, e0);
+                            store_coherent(cache + 1, e1);
+                        }
+                    }
+                }
+            }
+            tag++;
+            // K/V rows of earlier positions and the Wo rows stream into LDS
+            // while the q/k/v exchange completes.
+            __syncthreads();
+            if (pos > 0)
+                for (int kvh = 0; kvh < G::KVH; kvh++) {
+                    dma(kst + kvh * G::NP * G::HD, kc + size_t(kvh) * a.max_seq * G::HD,
+                        pos * G::HD * 4);
+                    dma(vst + kvh * G::NP * G::HD, vc + size_t(kvh) * a.max_seq * G::HD,
+                        pos * G::HD * 4);
+                }
+            stage_wo(l);
+            mark(it, 3 + 9 * l);
+
+            // ---------------------------- phase B: attention + Wo + residual --
+            // (take also completes the phase-A K/V stores of this wave before
+            // anything later is published)
+            take<G::DIM + 2 * G::KVD, false>(a.x_qkv, qkv, tag - 1, error);
+            for (int i = threadIdx.x; i < 2 * G::KVD; i += kThreads) {
+                const int which = i >= G::KVD;
+                const int j = i - which * G::KVD;
+                const int kvh = j / G::HD, d = j - kvh * G::HD;
+                (which ? vst : kst)[(kvh * G::NP + pos) * G::HD + d] = qkv[G::DIM + i];
+            }
+            __syncthreads();
+            mark(it, 4 + 9 * l);
+            {
+                const int n = pos + 1;
+                constexpr int Q4 = G::HD / 4;   // float4 per K/V row
+                constexpr int PG = kWave / Q4;  // positions per wave pass
+                const int d4 = lane % Q4, pg = lane / Q4;
+                float *sc = scores + wave * G::HPW * G::NP;
+                const int head0 = wave * G::HPW;
+                // scores: Q4 lanes per position, reduced by shuffles
+                for (int p0 = 0; p0 < n; p0 += PG) {
+                    const int p = p0 + pg;
+#pragma unroll
+                    for (int hh = 0; hh < G::HPW; hh++) {
+                        const int kvh = (head0 + hh) / G::GROUP;
+                        float part = 0.0f;
+                        if (p < n) {
+                            const float4 k = reinterpret_cast<const float4 *>(
+                                kst + (kvh * G::NP + p) * G::HD)[d4];
+                            const float4 q = reinterpret_cast<const float4 *>(
+                                qkv + (head0 + hh) * G::HD)[d4];
+                            part = fmaf(q.x, k.x, fmaf(q.y, k.y, fmaf(q.z, k.z, q.w * k.w)));
+                        }
+                        static_assert(Q4 == 16, "one DPP row per position");
+                        part = row16_sum(part);
+                        if (p < n && d4 == 0)
+                            sc[hh * G::NP + p] = part * a.attn_scale;
+                    }
+                }
+                // softmax per head (wave-local scores)
+                float total[G::HPW];
+#pragma unroll
+                for (int hh = 0; hh < G::HPW; hh++) {
+                    float m = -INFINITY;
+                    for (int p = lane; p < n; p += kWave)
+                        m = fmaxf(m, sc[hh * G::NP + p]);
+                    m = wave_maximum(m);
+                    float s = 0.0f;
+                    for (int p = lane; p < n; p += kWave) {
+                        const float e = expf(sc[hh * G::NP + p] - m);
+                        sc[hh * G::NP + p] = e;
+                        s += e;
+                    }
+                    total[hh] = wave_total(s);
+                }
+                // context: lane <-> (quad d4 of the row, head hh of the wave)
+                {
+                    static_assert(G::HPW * Q4 == kWave, "one DPP row per head");
+                    const int hh = lane / Q4;
+                    const int kvh = (head0 + hh) / G::GROUP;
+                    const float4 *vcol = reinterpret_cast<const float4 *>(
+                        vst + kvh * G::NP * G::HD) + d4;
+                    const float *w = sc + hh * G::NP;
+                    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    for (int p = 0; p < n; p++) {
+                        const float4 v = vcol[p * Q4];
+                        const float wgt = w[p];
+                        acc.x = fmaf(wgt, v.x, acc.x);
+                        acc.y = fmaf(wgt, v.y, acc.y);
+                        acc.z = fmaf(wgt, v.z, acc.z);
+                        acc.w = fmaf(wgt, v.w, acc.w);
+                    }
+                    float tot = total[0];
+#pragma unroll
+                    for (int h = 1; h < G::HPW; h++)
+                        if (hh == h)
+                            tot = total[h];
+                    const float inv = 1.0f / tot;
+                    const int e0 = (head0 + hh) * G::HD + 4 * d4;
+                    xs[swz(e0)] = acc.x * inv;
+                    xs[swz(e0 + 1)] = acc.y * inv;
+                    xs[swz(e0 + 2)] = acc.z * inv;
+                    xs[swz(e0 + 3)] = acc.w * inv;
+                }
+            }
+            __syncthreads();
+            block_sums(xs, xsum, G::DIM);
+            mark(it, 5 + 9 * l);
+            for (int r = wave; r < wo_e - wo_b; r += kWaves) {
+                const uint8_t *d;
+                const uint16_t *s;
+                slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
+                const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xs, xsum, G::BLK_DIM);
+                if (lane == 0)
+                    put(a.x_hidden + wo_b + r, h_raw[wo_b + r] + y, tag);
+            }
+            tag++;
+            // every wave is past attention (region 1) and past its reads of
+            // h_raw, which phase C's take overwrites
+            __syncthreads();
+            stage_gu(l);
+            mark(it, 6 + 9 * l);
+
+            // ------------------------------------------ phase C: gate/up --
+            sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
+            stage_x(h_raw, w.ffn_norm, rms_scale(wg_sum(sq, red), G::DIM), xs,
+                    xsum, G::DIM);
+            mark(it, 7 + 9 * l);
+            {
+                XRegs<G::CPL_DIM> x;
+                load_x(x, xs, xsum, G::BLK_DIM);
+                for (int pair = wave; pair < gu_e - gu_b; pair += kWaves) {
+                    const uint8_t *dg, *du;
+                    const uint16_t *sg, *su;
+                    slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, pair, dg, sg, r1);
+                    slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, G::ROWS_GU / 2 + pair, du, su, r1);
+                    const float g = row_dot<G::QT>(dg, sg, x, G::BLK_DIM);
+                    const float u = row_dot<G::QT>(du, su, x, G::BLK_DIM);
+                    if (lane == 0)
+                        put(a.x_act + gu_b + pair, g / (1.0f + expf(-g)) * u, tag);
+                }
+            }
+            tag++;
+            __syncthreads();
+            stage_down(l);
+            mark(it, 8 + 9 * l);
+
+            // --------------------------------------------- phase D: down --
+            take<G::FFN, true>(a.x_act, xs, tag - 1, error);
+            block_sums(xs, xsum, G::FFN);
+            mark(it, 9 + 9 * l);
+            {
+                const bool last = l + 1 == a.layer_count;
+                for (int r = wave; r < dn_e - dn_b; r += kWaves) {
+                    const uint8_t *d;
+                    const uint16_t *s;
+                    slot(G::ROWS_DN, G::RB_FFN, G::SB_FFN, r, d, s, r1);
+                    const float y = row_dot_lds<G::QT, G::CPL_FFN>(d, s, xs, xsum, G::BLK_FFN);
+                    if (lane == 0) {
+                        const float v = h_raw[dn_b + r] + y;
+                        put(a.x_hidden + dn_b + r, v, tag);
+                        if (last && it + 1 == a.n_iter)
+                            a.hidden_out[dn_b + r] = v;
+                    }
+                }
+                __syncthreads();
+                if (!last)
+                    stage_qkv(l + 1);
+            }
+            hidden_tag = tag;
+            tag++;
+            mark(it, 10 + 9 * l);
+        }
+        if (wg_failed(error, misc + 8))
+            break;
+    }
+    // hidden_out after an early stop (eos): the state the loop ended with
+    if (done && hidden_tag != 0) {
+        take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
+        for (int i = threadIdx.x; i < G::DIM; i += kThreads)
+            if (blockIdx.x == 0)
+                a.hidden_out[i] = h_raw[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.state->count = count;
+        a.state->done = done;
+        a.state->token = last_token;
+    }
+}
+
+using TinyLlamaInt4 = Geo<1, 2048, 5632, 32, 4, 64, 48>;
+using TinyLlamaInt8 = Geo<0, 2048, 5632, 32, 4, 64, 44>;
+
+template <class G>
+bool shape_is(const DecodeShape &s, int type)
+{
+    return type == G::QT && s.dim == G::DIM && s.ffn_dim == G::FFN &&
+           s.heads == G::HEADS && s.kv_heads == G::KVH && s.head_dim == G::HD;
+}
+
+int device_cus()
+{
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    int cus = 0;
+    hip_check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount,
+                                    device),
+              "hipDeviceGetAttribute");
+    return cus;
+}
+
+template <class G>
+void launch(const TokenArgs &args, hipStream_t stream)
+{
+    const auto kernel = token_kernel<G>;
+    hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  int(Lds<G>::BYTES)),
+              "hipFuncSetAttribute");
+    int per_cu = 0;
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                  &per_cu, reinterpret_cast<const void *>(kernel), kThreads,
+                  Lds<G>::BYTES),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    require(per_cu >= 1 && device_cus() >= kGrid, NUT_EDEVICE,
+            "token kernel: grid does not fit the device");
+    require(args.start_len + args.n_iter <= G::NP, NUT_EINVAL,
+            "token kernel: context exceeds the fused attention pass");
+    TokenArgs a = args;
+    void *params[] = {&a};
+    hip_check(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kernel),
+                                         dim3(kGrid), dim3(kThreads), params,
+                                         Lds<G>::BYTES, stream),
+              "token kernel launch");
+}
+
+} // namespace
+
+bool token_kernel_supported(int type, const DecodeShape &s)
+{
+    if (!(shape_is<TinyLlamaInt4>(s, type) || shape_is<TinyLlamaInt8>(s, type)))
+        return false;
+    return device_cus() >= kGrid;
+}
+
+int token_kernel_max_positions(int type, const DecodeShape &s)
+{
+    if (shape_is<TinyLlamaInt4>(s, type))
+        return TinyLlamaInt4::NP;
+    if (shape_is<TinyLlamaInt8>(s, type))
+        return TinyLlamaInt8::NP;
+    return 0;
+}
+
+size_t token_exchange_entries(const DecodeShape &s)
+{
+    const size_t kvd = size_t(s.kv_heads) * s.head_dim;
+    return (s.dim + 2 * kvd) + s.dim + s.ffn_dim + 2 * kGrid;
+}
+
+void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,
+                         hipStream_t stream)
+{
+    if (shape_is<TinyLlamaInt4>(s, type))
+        launch<TinyLlamaInt4>(a, stream);
+    else if (shape_is<TinyLlamaInt8>(s, type))
+        launch<TinyLlamaInt8>(a, stream);
+    else
+        fail(NUT_EINVAL, "token kernel: unsupported shape");
+}
+
+} // namespace nut

@@ -1,0 +1,58 @@
+// persistent.hpp — host interface of the cooperative token-loop kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+
+namespace nut {
+
+// Arguments of one launch. The kernel runs n_iter iterations; with
+// classify set, each iteration first runs the final rmsnorm + classifier +
+// argmax on the current hidden state (the generate loop), otherwise it
+// decodes tokens_in[it] (the prefill loop). Iteration it decodes at KV
+// position start_len + it.
+struct TokenArgs {
+    const LayerView *layers; // device array [layers]
+    const float *embeddings, *final_norm, *classifier;
+    const float2 *rope;
+    float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
+    uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
+    const float *hidden_in;   // hidden state before iteration 0 (classify)
+    float *hidden_out;        // hidden state after the last decode step
+    const int *tokens_in;     // per-iteration tokens (prefill)
+    int *tokens_out;          // emitted tokens (generate)
+    StepState *state;
+    int *error;               // set on a bounded-wait timeout
+    unsigned tag_base;        // unique per launch (launch counter << 20)
+    // Optional phase timeline of workgroup 0 (s_memrealtime ticks, 100 MHz):
+    // marks_per_iteration(layers) entries per iteration.
+    unsigned long long *timeline;
+    int timeline_cap;
+    int layer_count, vocab, max_seq, eos;
+    int start_len, n_iter, classify;
+    float attn_scale;
+};
+
+// Timeline entries per iteration: iteration start, token known, then per
+// layer: A input staged, A published, B input, attention done, B published,
+// C input, C published, D input, D published.
+__host__ __device__ inline int marks_per_iteration(int layers)
+{
+    return 2 + 9 * layers;
+}
+
+// Longest context (positions) the kernel's fused attention phase handles
+// for this shape; 0 when the shape has no instantiation.
+int token_kernel_max_positions(int type, const DecodeShape &s);
+
+// True when the cooperative kernel has an instantiation for this shape and
+// quant type and the device can hold its grid.
+bool token_kernel_supported(int type, const DecodeShape &s);
+// Exchange-buffer sizes (uint64 entries).
+size_t token_exchange_entries(const DecodeShape &s);
+void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,
+                         hipStream_t stream);
+
+} // namespace nut

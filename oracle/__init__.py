@@ -81,6 +81,7 @@ _REF = {
     "ref_silu": (C.c_float, [C.c_float]),
     "ref_model_create": (C.c_int, [_P, C.c_int, C.c_int, _P, _P, _P, _P]),
     "ref_model_add_layer": (C.c_int, [_P] * 10),
+    "ref_model_add_layer_quantized": (C.c_int, [_P] * 5),
     "ref_model_free": (None, [_P]),
     "ref_model_storage_bytes": (_SZ, [_P]),
     "ref_decode_trace": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
@@ -265,6 +266,35 @@ class RefModel:
                 self.handle, *[ptr(np.ascontiguousarray(w[n], np.float32))
                                for n in PROJECTIONS], ptr(an), ptr(fn)),
                 "ref_model_add_layer")
+
+    @classmethod
+    def from_quantized(cls, synth):
+        """Reference model over a SynthModel's quantised storage (its
+        quantiser is bit-identical to the reference's)."""
+        self = cls.__new__(cls)
+        c = synth.config
+        cfg_dict = {n: getattr(c, n) for n, _ in OrcConfig._fields_}
+        cfg = (C.c_size_t * 9)(*[cfg_dict[n] for n, _ in OrcConfig._fields_])
+        h = C.c_void_p()
+        check(ref().ref_model_create(cfg, synth.qtype, 0,
+                                     ptr(synth.embeddings),
+                                     ptr(synth.final_norm),
+                                     ptr(synth.lm_head), C.byref(h)),
+              "ref_model_create")
+        self.handle = h
+        self.dim = c.dim
+        self.vocab = c.vocab_size
+        ones = np.ones(c.dim, np.float32)
+        for mats in synth.layers:
+            data = (C.c_void_p * 7)(*[mats[n][0].ctypes.data
+                                      for n in PROJECTIONS])
+            scales = (C.c_void_p * 7)(*[mats[n][1].ctypes.data
+                                        for n in PROJECTIONS])
+            check(ref().ref_model_add_layer_quantized(self.handle, data,
+                                                      scales, ptr(ones),
+                                                      ptr(ones)),
+                  "ref_model_add_layer_quantized")
+        return self
 
     def decode_trace(self, tokens, threads=1, kv_elements=None):
         t = np.ascontiguousarray(tokens, np.int32)

@@ -205,6 +205,39 @@ int ref_model_add_layer(void *handle, const float *query, const float *key,
     GUARD_END
 }
 
+/* Append one layer from already-quantised storage (bytes + fp16 scale bits
+ * in the reference layout, e.g. from a quantiser shown bit-identical to
+ * QuantizedMatrix::quantize). mats[i] = {data, scales} for query, key,
+ * value, output, gate, up, down. */
+int ref_model_add_layer_quantized(void *handle, const void *const *data,
+                                  const void *const *scales,
+                                  const float *attention_norm,
+                                  const float *ffn_norm)
+{
+    GUARD_BEGIN
+    QuantizedModelWeights &m = *static_cast<RefModel *>(handle)->weights;
+    const ModelConfig &c = m.config;
+    const size_t shapes[7][2] = {{c.dim, c.dim},     {c.kv_dim(), c.dim},
+                                 {c.kv_dim(), c.dim}, {c.dim, c.dim},
+                                 {c.ffn_dim, c.dim}, {c.ffn_dim, c.dim},
+                                 {c.dim, c.ffn_dim}};
+    std::vector<QuantizedMatrix> mats;
+    for (int i = 0; i < 7; i++) {
+        QuantizedMatrix q(shapes[i][0], shapes[i][1], 32, m.quant_type);
+        std::memcpy(q.data_.data(), data[i], q.data_.size());
+        std::memcpy(q.scales_.data(), scales[i],
+                    q.scales_.size() * sizeof(uint16_t));
+        mats.push_back(std::move(q));
+    }
+    m.layers.emplace_back(std::move(mats[0]), std::move(mats[1]),
+                          std::move(mats[2]), std::move(mats[3]),
+                          std::move(mats[4]), std::move(mats[5]),
+                          std::move(mats[6]),
+                          std::vector<float>(attention_norm, attention_norm + c.dim),
+                          std::vector<float>(ffn_norm, ffn_norm + c.dim));
+    GUARD_END
+}
+
 void ref_model_free(void *handle) { delete static_cast<RefModel *>(handle); }
 
 size_t ref_model_storage_bytes(void *handle)

@@ -192,3 +192,46 @@ def test_tinyllama_int4_greedy_16(gpu):
     om.reset()
     assert rel_l2(h, om.prefill(prompt)) <= TOL
     dev.close()
+
+
+@pytest.fixture(scope="module")
+def tinyllama_int4(gpu):
+    O.orc().orc_set_threads(16)
+    model, prompt, gen = W.build_run("tinyllama_int4")
+    dev = model.to_device()
+    yield model, prompt, gen, dev
+    dev.close()
+
+
+@pytest.mark.parametrize("path", [1, 2], ids=["steps", "token"])
+def test_tinyllama_int4_paths_greedy(gpu, tinyllama_int4, path):
+    """Step kernels and the cooperative token kernel both reproduce the
+    oracle's 16 greedy ids and its post-prompt hidden state."""
+    model, prompt, gen, dev = tinyllama_int4
+    dev.set_path(path)
+    ids, stats = dev.generate(prompt, gen)
+    om = O.oracle_model(model)
+    ref, _, _ = om.generate(prompt, gen)
+    assert ids == ref
+    cache = gpu.KVCache(model.config)
+    h = dev.prefill(cache, prompt)
+    om.reset()
+    assert rel_l2(h, om.prefill(prompt)) <= TOL
+    # one more decode step on the same cache, and its K/V rows
+    h2 = dev.decode(cache, ref[0])
+    assert rel_l2(h2, om.decode(ref[0])) <= TOL
+    pos = len(prompt)
+    for layer in (0, model.config.layers - 1):
+        for head in range(model.config.kv_heads):
+            k, v = cache.key_value(layer, head, pos)
+            rk, rv = om.kv_row(layer, head, pos)
+            assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+    dev.set_path(0)
+
+
+def test_token_kernel_rejects_unsupported_shape(gpu, tiny):
+    model, prompt, _, dev = tiny
+    dev.set_path(2)
+    with pytest.raises(gpu.InvalidArgument, match="token kernel"):
+        dev.generate(prompt, 4)
+    dev.set_path(0)
