@@ -210,14 +210,16 @@ enum { NUT_PATH_AUTO = 0, NUT_PATH_STEPS = 1, NUT_PATH_TOKEN = 2 };
 int nut_model_set_path(nut_model *m, int path);
 
 /* Phase timeline of the cooperative token kernel, for profiling (no
- * reference counterpart): when enabled, workgroup 0 stamps the device's
- * constant 100 MHz clock at each phase boundary; per decode iteration
- * 2 + 9 * layers entries: iteration start, token known, then per layer the
- * times its QKV input is staged, QKV published, attention input staged,
- * attention done, Wo published, FFN input staged, gate/up published, down
- * input staged and down published. nut_model_timeline copies up to
- * capacity entries of the last launch's timeline. */
-int nut_model_record_timeline(nut_model *m, int enable);
+ * reference counterpart). mode 0 records nothing, 1 workgroup 0, 2 every
+ * workgroup of the grid (256): each stamps the device's constant 100 MHz
+ * clock at each phase boundary; per decode iteration 2 + 9 * layers
+ * entries: iteration start, token known, then per layer the times its QKV
+ * input is staged, QKV published, attention input staged, attention done,
+ * Wo published, FFN input staged, gate/up published, down input staged and
+ * down published. Entries are [workgroup][max_seq iterations][marks].
+ * nut_model_timeline copies up to capacity entries of the last launch's
+ * timeline. */
+int nut_model_record_timeline(nut_model *m, int mode);
 int nut_model_timeline(const nut_model *m, uint64_t *ticks, size_t capacity,
                        size_t *count);
 

@@ -449,19 +449,26 @@ class DeviceModel:
         """0 auto, 1 per-phase step kernels, 2 cooperative token kernel."""
         check(lib().nut_model_set_path(self.handle, path))
 
-    def record_timeline(self, enable=True):
-        check(lib().nut_model_record_timeline(self.handle, int(enable)))
+    def record_timeline(self, mode=1):
+        """0 off, 1 workgroup 0 (True), 2 every workgroup."""
+        check(lib().nut_model_record_timeline(self.handle, int(mode)))
+        self._timeline_wgs = {0: 0, 1: 1, 2: 256}[int(mode)]
 
     def timeline(self, iterations):
         """Phase timeline of the last token-kernel launch, in microseconds
-        from its first mark: array [iterations, 2 + 9 * layers]."""
+        from workgroup 0's first mark: array [iterations, 2 + 9 * layers],
+        or [workgroups, iterations, marks] when every workgroup records."""
         marks = 2 + 9 * self.config.layers
-        out = np.zeros(iterations * marks, np.uint64)
+        wgs = getattr(self, "_timeline_wgs", 1)
+        per = self.config.max_seq * marks
+        out = np.zeros(max(wgs, 1) * per, np.uint64)
         n = C.c_size_t()
         check(lib().nut_model_timeline(self.handle, _ptr(out), out.size,
                                        C.byref(n)))
-        t = out[:n.value].astype(np.float64).reshape(-1, marks)
-        return (t - t[0, 0]) / 100.0  # 100 MHz ticks -> us
+        t = out[:n.value].astype(np.float64).reshape(-1, self.config.max_seq, marks)
+        t = t[:, :iterations]
+        t = (t - t[0, 0, 0]) / 100.0  # 100 MHz ticks -> us
+        return t[0] if wgs == 1 else t
 
     def last_decode_ms(self):
         """Device time of the last generate() decode loop (HIP events)."""

@@ -264,21 +264,24 @@ int nut_model_set_path(nut_model *m, int path)
     });
 }
 
-int nut_model_record_timeline(nut_model *m, int enable)
+int nut_model_record_timeline(nut_model *m, int mode)
 {
     return nut::guarded([&]() {
         nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::require(mode >= 0 && mode <= 2, NUT_EINVAL, "timeline: unknown mode");
         nut::ensure_device();
-        if (enable) {
-            const size_t n = m->config.max_seq *
+        m->timeline.release();
+        m->timeline_entries = 0;
+        m->timeline_wgs = 0;
+        if (mode != 0) {
+            const int wgs = mode == 1 ? 1 : nut::kTokenGrid;
+            const size_t n = size_t(wgs) * m->config.max_seq *
                              size_t(nut::marks_per_iteration(int(m->config.layers)));
             m->timeline.allocate(n * sizeof(unsigned long long));
             nut::hip_check(hipMemset(m->timeline.get(), 0, n * sizeof(unsigned long long)),
                            "hipMemset");
             m->timeline_entries = n;
-        } else {
-            m->timeline.release();
-            m->timeline_entries = 0;
+            m->timeline_wgs = wgs;
         }
     });
 }

@@ -123,6 +123,8 @@ nut_model *create_model(const nut_config &config, int type, bool tied)
     m->type = type;
     m->tied = tied;
     m->shape = shape_of(config);
+    m->layout = layer_layout(type, config.dim, config.ffn_dim,
+                             kv_heads_of(config) * config.head_dim);
     m->layers.resize(config.layers);
     const size_t dim = config.dim, vocab = config.vocab_size;
     m->embeddings.allocate(vocab * dim * sizeof(float));
@@ -178,6 +180,7 @@ void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
                                  {c.dim, c.ffn_dim}};
     size_t offsets[7][2];
     size_t total = 0, accounted = 0;
+    bool blocks32 = true;
     for (int i = 0; i < 7; i++) {
         const nut_qmatrix *q = mats[i];
         require(q != nullptr && q->data != nullptr && q->scales != nullptr,
@@ -193,13 +196,29 @@ void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
         offsets[i][1] = total;
         total = align_up(total + scales);
         accounted += data + scales;
+        blocks32 = blocks32 && q->block_size == 32;
     }
-    const size_t norms = total;
+    size_t norms = total;
     total += 2 * c.dim * sizeof(float);
     DeviceLayer &dl = m.layers[layer];
     dl.storage.release();
-    dl.storage.allocate(total);
-    uint8_t *base = dl.storage.as<uint8_t>();
+    uint8_t *base;
+    if (blocks32) {
+        // Same offsets as layer_layout (checked), inside the arena.
+        const LayerLayout &lay = m.layout;
+        for (int i = 0; i < 7; i++)
+            require(offsets[i][0] == lay.data[i] && offsets[i][1] == lay.scales[i],
+                    NUT_EINVAL, "quantized model: arena layout mismatch");
+        require(norms == lay.attention_norm, NUT_EINVAL,
+                "quantized model: arena layout mismatch");
+        if (m.arena.get() == nullptr)
+            m.arena.allocate(lay.bytes * c.layers);
+        base = m.arena.as<uint8_t>() + layer * lay.bytes;
+    } else {
+        dl.storage.allocate(total);
+        base = dl.storage.as<uint8_t>();
+    }
+    dl.in_arena = blocks32;
     QMat views[7];
     for (int i = 0; i < 7; i++) {
         const nut_qmatrix *q = mats[i];
@@ -283,7 +302,10 @@ bool use_token_kernel(nut_model &m, size_t end_length)
 {
     if (m.path == 1)
         return false;
-    const bool ok = token_kernel_supported(m.type, m.shape) &&
+    bool arena = true;
+    for (const DeviceLayer &l : m.layers)
+        arena = arena && l.in_arena;
+    const bool ok = arena && token_kernel_supported(m.type, m.shape) &&
                     end_length <= size_t(token_kernel_max_positions(m.type, m.shape));
     if (m.path == 2 && !ok)
         fail(NUT_EINVAL, "token kernel: shape or context not supported");
@@ -292,12 +314,7 @@ bool use_token_kernel(nut_model &m, size_t end_length)
 
 void prepare_token_kernel(nut_model &m)
 {
-    if (m.layer_views.get() == nullptr) {
-        std::vector<LayerView> views;
-        for (const DeviceLayer &l : m.layers)
-            views.push_back(l.view);
-        m.layer_views.allocate(views.size() * sizeof(LayerView));
-        upload(m.layer_views.get(), views.data(), views.size() * sizeof(LayerView));
+    if (m.exchange.get() == nullptr) {
         const size_t entries = token_exchange_entries(m.shape);
         m.exchange.allocate(entries * sizeof(uint64_t));
         hip_check(hipMemset(m.exchange.get(), 0, entries * sizeof(uint64_t)), "hipMemset");
@@ -315,7 +332,7 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     const size_t kvd = size_t(s.kv_heads) * s.head_dim;
     uint64_t *x = m.exchange.as<uint64_t>();
     TokenArgs a{};
-    a.layers = m.layer_views.as<LayerView>();
+    a.weights = m.arena.as<uint8_t>();
     a.embeddings = m.embeddings.as<float>();
     a.final_norm = m.final_norm.as<float>();
     a.classifier = m.output_weights();
@@ -342,7 +359,8 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.classify = classify ? 1 : 0;
     a.attn_scale = s.attn_scale;
     a.timeline = m.timeline_entries > 0 ? m.timeline.as<unsigned long long>() : nullptr;
-    a.timeline_cap = int(m.timeline_entries);
+    a.timeline_wgs = m.timeline_wgs;
+    a.timeline_cap = m.timeline_wgs > 0 ? int(m.timeline_entries / m.timeline_wgs) : 0;
     launch_set_int(a.error, 0, m.stream);
     launch_token_kernel(m.type, s, a, m.stream);
 }

@@ -14,8 +14,11 @@ struct nut_kvcache;
 namespace nut {
 
 struct DeviceLayer {
-    DeviceBuffer storage; // 7 projections + 2 norms, 256-byte aligned
+    // Own storage of a layer whose blocks are not 32 wide; layers with
+    // 32-wide blocks live in the model's arena instead.
+    DeviceBuffer storage;
     LayerView view{};
+    bool in_arena = false;
     size_t storage_bytes = 0; // reference storage accounting
     bool set = false;
 };
@@ -48,6 +51,9 @@ struct nut_model {
     nut::DecodeShape shape{};
     std::vector<nut::DeviceLayer> layers;
     nut::DeviceBuffer embeddings, final_norm, lm_head, rope;
+    // Weight arena: layer l at arena + l * layout.bytes (LayerLayout).
+    nut::DeviceBuffer arena;
+    nut::LayerLayout layout{};
     bool globals_set = false;
 
     // Step workspace.
@@ -57,8 +63,9 @@ struct nut_model {
     hipEvent_t decode_begin = nullptr, decode_end = nullptr;
     // Cooperative token kernel state.
     int path = 0; // 0 auto, 1 step kernels, 2 token kernel
-    nut::DeviceBuffer layer_views, exchange, token_error, timeline;
+    nut::DeviceBuffer exchange, token_error, timeline;
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
+    int timeline_wgs = 0;        // workgroups it covers
     unsigned launch_count = 0;
     double last_decode_device_ms = 0.0; // events around the decode loop
     std::unique_ptr<nut_kvcache> generation_cache;

@@ -28,7 +28,7 @@ namespace nut {
 
 namespace {
 
-constexpr int kGrid = 256;
+constexpr int kGrid = kTokenGrid;
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kSpinLimit = 200000;
@@ -64,6 +64,8 @@ struct Geo {
     static constexpr int W_WO = ROWS_WO * (RB_DIM + SB_DIM);
     static constexpr int R1 = cmax(cmax(KV_BYTES, W_QKV), cmax(W_GU, W_DN));
     static constexpr int R2 = W_WO;
+    // weight arena layout of one layer
+    static constexpr LayerLayout LAY = layer_layout(QT, DIM, FFN, KVD);
     static_assert(DIM % 32 == 0 && FFN % 32 == 0, "block-aligned rows");
     static_assert(RB_FFN % 16 == 0 && SB_FFN % 16 == 0 && SB_DIM % 16 == 0,
                   "16-byte DMA granules");
@@ -209,14 +211,48 @@ __device__ void block_sums(const float *xs, float *xsum, int n)
     __syncthreads();
 }
 
+// This thread's elements i = threadIdx.x + kThreads * u of an N-vector in
+// global memory, in registers; loads issued together (no dependent waits).
+template <int N> struct Slice {
+    static constexpr int PER = cdiv(N, kThreads);
+    float v[PER];
+    __device__ __forceinline__ void load(const float *src)
+    {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = threadIdx.x + u * kThreads;
+            v[u] = i < N ? src[i] : 0.0f;
+        }
+    }
+    // dst[i] = v, returns this thread's sum of squares.
+    __device__ __forceinline__ float store(float *dst) const
+    {
+        float sq = 0.0f;
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int i = threadIdx.x + u * kThreads;
+            if (i < N) {
+                dst[i] = v[u];
+                sq = fmaf(v[u], v[u], sq);
+            }
+        }
+        return sq;
+    }
+};
+
 // xs (swizzled) = src * scale * w, plus block sums; ends with a barrier.
-__device__ void stage_x(const float *src, const float *weight, float scale,
-                        float *xs, float *xsum, int n)
+template <int N>
+__device__ void stage_x(const float *src, const Slice<N> &w, float scale,
+                        float *xs, float *xsum)
 {
-    for (int i = threadIdx.x; i < n; i += kThreads)
-        xs[swz(i)] = src[i] * scale * weight[i];
+#pragma unroll
+    for (int u = 0; u < Slice<N>::PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < N)
+            xs[swz(i)] = src[i] * scale * w.v[u];
+    }
     __syncthreads();
-    block_sums(xs, xsum, n);
+    block_sums(xs, xsum, N);
 }
 
 __device__ __forceinline__ float rms_scale(float squares, int n)
@@ -224,9 +260,12 @@ __device__ __forceinline__ float rms_scale(float squares, int n)
     return 1.0f / sqrtf(squares / float(n) + 1e-5f);
 }
 
-// dst[map(i)] = value of src[i] once tagged, i < N (all loads issued before
-// the first tag test: one coherent round trip); returns this thread's sum of
-// squares. Waits for this wave's outstanding DMA, then a barrier.
+// dst[map(i)] = value of src[i] once tagged, i < N; returns this thread's
+// sum of squares. A thread's loads are issued together, and every round
+// re-issues all of its still-stale loads together, so a late producer costs
+// one coherent round trip per round rather than one per element. Bounded:
+// gives up once any wait failed. Waits for this wave's outstanding DMA, then
+// a barrier.
 template <int N, bool SWIZZLE>
 __device__ float take(const uint64_t *src, float *dst, unsigned tag,
                       int *error)
@@ -236,15 +275,33 @@ __device__ float take(const uint64_t *src, float *dst, unsigned tag,
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = threadIdx.x + u * kThreads;
-        v[u] = i < N ? load_coherent(src + i) : 0;
+        v[u] = i < N ? load_coherent(src + i) : uint64_t(tag) << 32;
+    }
+    for (int spins = 0;; spins++) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            stale |= unsigned(v[u] >> 32) != tag;
+        if (!stale)
+            break;
+        if ((spins & 63) == 63 && failed(error))
+            break;
+        if (spins > kSpinLimit) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            if (unsigned(v[u] >> 32) != tag)
+                v[u] = load_coherent(src + threadIdx.x + u * kThreads);
     }
     float squares = 0.0f;
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const int i = threadIdx.x + u * kThreads;
         if (i < N) {
-            if (unsigned(v[u] >> 32) != tag)
-                v[u] = wait_tag(src + i, tag, error);
             const float f = __uint_as_float(unsigned(v[u]));
             dst[SWIZZLE ? swz(i) : i] = f;
             squares = fmaf(f, f, squares);
@@ -375,32 +432,11 @@ __device__ __forceinline__ float row_dot_lds(const uint8_t *row,
     return wave_total(acc);
 }
 
-__device__ __forceinline__ const uint8_t *row_data(const QMat &m, int row)
-{
-    return m.data + size_t(row) * (m.type == 1 ? m.cols / 2 : m.cols);
-}
-
-__device__ __forceinline__ const uint16_t *row_scales(const QMat &m, int row)
-{
-    return m.scales + size_t(row) * (m.cols / 32);
-}
-
 // Units [begin, end) of `units` owned by this workgroup.
 __device__ __forceinline__ void wg_share(int units, int &begin, int &end)
 {
     begin = int((long long)units * blockIdx.x / kGrid);
     end = int((long long)units * (blockIdx.x + 1) / kGrid);
-}
-
-// DMA rows [lo, hi) of m into LDS row slots starting at slot `first`.
-template <int RB, int SB, int ROWS>
-__device__ __forceinline__ void stage_rows(uint8_t *region, const QMat &m,
-                                           int lo, int hi, int first)
-{
-    if (hi <= lo)
-        return;
-    dma(region + first * RB, row_data(m, lo), (hi - lo) * RB);
-    dma(region + ROWS * RB + first * SB, row_scales(m, lo), (hi - lo) * SB);
 }
 
 // ------------------------------------------------------------- kernel --
@@ -441,12 +477,14 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     int *error = a.error;
     const size_t kv_layer = size_t(G::KVH) * a.max_seq * G::HD;
     const int marks = marks_per_iteration(a.layer_count);
-    // Phase timeline: workgroup 0 stamps entry k of iteration `it`.
+    // Phase timeline: recorded workgroups stamp entry k of iteration `it`.
     auto mark = [&](int it, int k) {
-        if (a.timeline != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+        if (a.timeline != nullptr && int(blockIdx.x) < a.timeline_wgs &&
+            threadIdx.x == 0) {
             const int i = it * marks + k;
             if (i < a.timeline_cap)
-                a.timeline[i] = __builtin_amdgcn_s_memrealtime();
+                a.timeline[size_t(blockIdx.x) * a.timeline_cap + i] =
+                    __builtin_amdgcn_s_memrealtime();
         }
     };
 
@@ -456,32 +494,51 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     wg_share(G::FFN, gu_b, gu_e); // (gate, up) pairs
     wg_share(G::DIM, dn_b, dn_e);
 
-    // Weight staging of each phase (region and slot layout).
+    // Weight staging of each phase (region and slot layout). Weights are
+    // addressed from the arena base alone, so staging issues no loads.
+    auto wdata = [&](int layer, int m) {
+        return a.weights + size_t(layer) * G::LAY.bytes + G::LAY.data[m];
+    };
+    auto wscales = [&](int layer, int m) {
+        return reinterpret_cast<const uint16_t *>(
+            a.weights + size_t(layer) * G::LAY.bytes + G::LAY.scales[m]);
+    };
+    auto stage = [&](uint8_t *region, int rows, int rb, int sb, int layer,
+                     int m, int lo, int hi, int first) {
+        if (hi <= lo)
+            return;
+        dma(region + first * rb, wdata(layer, m) + size_t(lo) * rb,
+            (hi - lo) * rb);
+        dma(region + rows * rb + first * sb,
+            reinterpret_cast<const uint8_t *>(wscales(layer, m)) +
+                size_t(lo) * sb,
+            (hi - lo) * sb);
+    };
     auto stage_qkv = [&](int layer) {
-        const LayerView &w = a.layers[layer];
         const int lo = 2 * qkv_b, hi = 2 * qkv_e;
         const int q_hi = G::DIM, k_hi = G::DIM + G::KVD;
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
-            r1, w.query, lo, min(hi, q_hi), 0);
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
-            r1, w.key, max(lo, q_hi) - q_hi, min(hi, k_hi) - q_hi,
-            max(lo, q_hi) - lo);
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_QKV>(
-            r1, w.value, max(lo, k_hi) - k_hi, hi - k_hi, max(lo, k_hi) - lo);
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 0, lo,
+              min(hi, q_hi), 0);
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 1,
+              max(lo, q_hi) - q_hi, min(hi, k_hi) - q_hi, max(lo, q_hi) - lo);
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 2,
+              max(lo, k_hi) - k_hi, hi - k_hi, max(lo, k_hi) - lo);
     };
     auto stage_wo = [&](int layer) {
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_WO>(r2, a.layers[layer].output,
-                                                     wo_b, wo_e, 0);
+        stage(r2, G::ROWS_WO, G::RB_DIM, G::SB_DIM, layer, 3, wo_b, wo_e, 0);
     };
     auto stage_gu = [&](int layer) {
-        const LayerView &w = a.layers[layer];
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_GU>(r1, w.gate, gu_b, gu_e, 0);
-        stage_rows<G::RB_DIM, G::SB_DIM, G::ROWS_GU>(r1, w.up, gu_b, gu_e,
-                                                     G::ROWS_GU / 2);
+        stage(r1, G::ROWS_GU, G::RB_DIM, G::SB_DIM, layer, 4, gu_b, gu_e, 0);
+        stage(r1, G::ROWS_GU, G::RB_DIM, G::SB_DIM, layer, 5, gu_b, gu_e,
+              G::ROWS_GU / 2);
     };
     auto stage_down = [&](int layer) {
-        stage_rows<G::RB_FFN, G::SB_FFN, G::ROWS_DN>(r1, a.layers[layer].down,
-                                                     dn_b, dn_e, 0);
+        stage(r1, G::ROWS_DN, G::RB_FFN, G::SB_FFN, layer, 6, dn_b, dn_e, 0);
+    };
+    auto norm = [&](int layer, bool ffn) {
+        return reinterpret_cast<const float *>(
+            a.weights + size_t(layer) * G::LAY.bytes +
+            (ffn ? G::LAY.ffn_norm : G::LAY.attention_norm));
     };
     auto slot = [&](int rows, int rb, int sb, int s, const uint8_t *&d,
                     const uint16_t *&sc, const uint8_t *region) {
@@ -499,22 +556,25 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         if (a.classify) {
             // ---------------- final rmsnorm + classifier + argmax ----
             const float *wcls = a.classifier;
+            Slice<G::DIM> nw;
+            nw.load(a.final_norm);
             float sq;
             if (hidden_tag == 0) {
-                sq = 0.0f;
-                for (int i = threadIdx.x; i < G::DIM; i += kThreads) {
-                    const float v = a.hidden_in[i];
-                    h_raw[i] = v;
-                    sq = fmaf(v, v, sq);
-                }
+                Slice<G::DIM> h;
+                h.load(a.hidden_in);
+                sq = h.store(h_raw);
                 __syncthreads();
             } else {
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
             }
             const float scale = rms_scale(wg_sum(sq, red), G::DIM);
             // plain layout: lane needs x[4c..4c+3], c = lane + 64 j
-            for (int i = threadIdx.x; i < G::DIM; i += kThreads)
-                xs[i] = h_raw[i] * scale * a.final_norm[i];
+#pragma unroll
+            for (int u = 0; u < Slice<G::DIM>::PER; u++) {
+                const int i = threadIdx.x + u * kThreads;
+                if (i < G::DIM)
+                    xs[i] = h_raw[i] * scale * nw.v[u];
+            }
             __syncthreads();
             constexpr int C4 = G::DIM / 4 / kWave; // float4 per lane per row
             const float4 *x4 = reinterpret_cast<const float4 *>(xs);
@@ -639,7 +699,6 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         mark(it, 1);
 
         for (int l = 0; l < a.layer_count; l++) {
-            const LayerView &w = a.layers[l];
             float *kc = a.k_cache + l * kv_layer;
             float *vc = a.v_cache + l * kv_layer;
 
@@ -652,21 +711,18 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 if (row < G::DIM + G::KVD)
                     rope_cs = a.rope[size_t(pos) * (G::HD / 2) + (local % G::HD) / 2];
             }
+            Slice<G::DIM> nw;
+            nw.load(norm(l, false));
             float sq;
             if (l == 0) {
-                sq = 0.0f;
-                const float *e = a.embeddings + size_t(token) * G::DIM;
-                for (int i = threadIdx.x; i < G::DIM; i += kThreads) {
-                    const float v = e[i];
-                    h_raw[i] = v;
-                    sq = fmaf(v, v, sq);
-                }
+                Slice<G::DIM> e;
+                e.load(a.embeddings + size_t(token) * G::DIM);
+                sq = e.store(h_raw);
                 dma_wait();
             } else {
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
             }
-            stage_x(h_raw, w.attention_norm, rms_scale(wg_sum(sq, red), G::DIM),
-                    xs, xsum, G::DIM);
+            stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
             mark(it, 2 + 9 * l);
             {
                 XRegs<G::CPL_DIM> x;
@@ -820,9 +876,9 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 6 + 9 * l);
 
             // ------------------------------------------ phase C: gate/up --
+            nw.load(norm(l, true));
             sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
-            stage_x(h_raw, w.ffn_norm, rms_scale(wg_sum(sq, red), G::DIM), xs,
-                    xsum, G::DIM);
+            stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
             mark(it, 7 + 9 * l);
             {
                 XRegs<G::CPL_DIM> x;

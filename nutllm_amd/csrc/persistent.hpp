@@ -8,13 +8,17 @@
 
 namespace nut {
 
+// Workgroups of the cooperative kernel (one per CU of an MI355X).
+constexpr int kTokenGrid = 256;
+
 // Arguments of one launch. The kernel runs n_iter iterations; with
 // classify set, each iteration first runs the final rmsnorm + classifier +
 // argmax on the current hidden state (the generate loop), otherwise it
 // decodes tokens_in[it] (the prefill loop). Iteration it decodes at KV
 // position start_len + it.
 struct TokenArgs {
-    const LayerView *layers; // device array [layers]
+    // Weight arena: layer l at weights + l * layer_layout(...).bytes.
+    const uint8_t *weights;
     const float *embeddings, *final_norm, *classifier;
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
@@ -26,10 +30,11 @@ struct TokenArgs {
     StepState *state;
     int *error;               // set on a bounded-wait timeout
     unsigned tag_base;        // unique per launch (launch counter << 20)
-    // Optional phase timeline of workgroup 0 (s_memrealtime ticks, 100 MHz):
-    // marks_per_iteration(layers) entries per iteration.
+    // Optional phase timeline (s_memrealtime ticks, 100 MHz) of workgroups
+    // [0, timeline_wgs): marks_per_iteration(layers) entries per iteration,
+    // timeline_cap entries per workgroup.
     unsigned long long *timeline;
-    int timeline_cap;
+    int timeline_cap, timeline_wgs;
     int layer_count, vocab, max_seq, eos;
     int start_len, n_iter, classify;
     float attn_scale;
