@@ -140,7 +140,8 @@ def quantize(w, qtype, block_size=32):
     rows, cols = w.shape
     n = rows * cols
     data = np.zeros(n if qtype == 0 else (n + 1) // 2, np.uint8)
-    scales = np.zeros((n + block_size - 1) // block_size, np.uint16)
+    scales = np.zeros(max(1, -(-n // block_size)) if block_size else 1,
+                      np.uint16)
     st = orc().orc_quantize(ptr(w), rows, cols, qtype, block_size, ptr(data),
                             ptr(scales))
     return st, data, scales

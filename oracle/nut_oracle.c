@@ -202,7 +202,11 @@ float orc_error_bound(const orc_qmat *m, size_t row, size_t column)
     if (half_rounding < 0x1p-25f)
         half_rounding = 0x1p-25f;
     const float limit = m->type == ORC_INT8 ? 127.0f : 7.0f;
-    return fmaf(limit + 0.5f, half_rounding, stored * 0.5f);
+    /* g++ -mfma contracts this sum as fma(stored, 0.5f, product): the
+     * (limit + 0.5) * half_rounding product is rounded on its own, and
+     * stored * 0.5f is exact, so the fma equals the plain sum below. */
+    const float product = (limit + 0.5f) * half_rounding;
+    return stored * 0.5f + product;
 }
 
 void orc_dequantize(const orc_qmat *m, float *out)

@@ -4,13 +4,19 @@ Bars (from the path's contract): quantisation bit-exact; matvec, attention,
 logits and hidden states within rel-L2 1e-5 (fp32 arithmetic); greedy token
 ids identical for the first 16 generated tokens.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
+import llama2c
 import oracle as O
 from nutllm_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 TOL = 1e-5  # rel-L2, fp32 paths
 
@@ -177,7 +183,8 @@ def test_decode_errors(gpu, tiny):
 
 
 def test_tinyllama_int4_greedy_16(gpu):
-    """Headline shape: 16 greedy ids identical to the oracle."""
+    """Headline shape: 16 greedy ids identical to the oracle's and to the
+    ids the reference generated (tests/golden/tinyllama_int4.json)."""
     O.orc().orc_set_threads(16)
     model, prompt, gen = W.build_run("tinyllama_int4")
     dev = model.to_device()
@@ -185,6 +192,10 @@ def test_tinyllama_int4_greedy_16(gpu):
     om = O.oracle_model(model)
     ref, _, _ = om.generate(prompt, gen)
     assert ids == ref
+    with open(os.path.join(GOLDEN, "tinyllama_int4.json")) as f:
+        golden = json.load(f)
+    assert golden["prompt"] == prompt.tolist()
+    assert ids == golden["ids"]
     assert len(ids) == 16 or 1 in ref
     # hidden state after the prompt
     cache = gpu.KVCache(model.config)
@@ -235,3 +246,46 @@ def test_token_kernel_rejects_unsupported_shape(gpu, tiny):
     with pytest.raises(gpu.InvalidArgument, match="token kernel"):
         dev.generate(prompt, 4)
     dev.set_path(0)
+
+
+@pytest.mark.parametrize("qtype", [0, 1], ids=["int8", "int4"])
+def test_llama2c_fixture_says_hi(gpu, qtype):
+    """The reference's llama2.c fixture (all-zero projections): prompt
+    [1, 0, 3] generates [4, 5] then eos (src/loader_selftest.cpp, file lines
+    81-116), through the device model and the product quantiser."""
+    cfg, w, _ = llama2c.load(os.path.join(GOLDEN, "tiny-llama2.bin"))
+    dev = gpu.DeviceModel(gpu.Config(**cfg), qtype)
+    dev.set_globals(np.ascontiguousarray(w["embeddings"]),
+                    np.ascontiguousarray(w["final_norm"]),
+                    np.ascontiguousarray(w["classifier"]))
+    for l in range(cfg["layers"]):
+        mats = {}
+        for name in O.PROJECTIONS:
+            m = np.ascontiguousarray(w[name][l])
+            data, scales = gpu.quantize(m, qtype)
+            mats[name] = (data, scales, m.shape[0], m.shape[1])
+        dev.set_layer(l, mats, np.ascontiguousarray(w["attention_norm"][l]),
+                      np.ascontiguousarray(w["ffn_norm"][l]))
+    ids, stats = dev.generate(np.array([1, 0, 3], np.int32), 8)
+    assert ids == [4, 5]
+    assert stats.prefill_tokens == 3 and stats.generated_tokens == 2
+    dev.close()
+
+
+@pytest.mark.parametrize("qtype,tag", [(0, "int8"), (1, "int4")])
+def test_tiny_matches_reference_golden(gpu, qtype, tag):
+    """Greedy ids equal the reference's; every decode step's hidden state
+    and the final-step logits within rel-L2 1e-5 of the reference's
+    (tests/golden/tiny_*.npz)."""
+    g = np.load(os.path.join(GOLDEN, f"tiny_{tag}.npz"))
+    model = W.build("tiny", qtype, 0)
+    dev = model.to_device()
+    ids, _ = dev.generate(g["prompt"], 16)
+    assert ids == g["ids"].tolist()
+    cache = gpu.KVCache(model.config)
+    for i, token in enumerate(g["tokens"]):
+        h = dev.decode(cache, int(token))
+        assert rel_l2(h, g["hidden"][i]) <= TOL, f"step {i}"
+    logits = dev.logits(g["hidden"][len(g["prompt"]) - 1])
+    assert rel_l2(logits, g["logits"]) <= TOL
+    dev.close()
