@@ -32,6 +32,12 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 
+# HBM bytes one generate launch (16 iterations) moves, from rocprofv3
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (scales from a 1 GiB device copy);
+# profiles/token_kernel_tinyllama_int4_decode.md holds the runs.
+MEASURED_TRAFFIC_BYTES = 13_523_878_912
+CPU_SAMPLE_SECONDS = 10.0
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -56,18 +62,23 @@ def cpu_baseline(model, prompt, gen):
         run = lambda: om.generate(prompt, gen)  # noqa: E731
     rates, prefill = [], []
     ids = None
-    for _ in range(3):
+    start = time.perf_counter()
+    # repeat whole generate calls for about CPU_SAMPLE_SECONDS (at most 30)
+    while len(rates) < 30 and (len(rates) < 2 or time.perf_counter() - start
+                               < CPU_SAMPLE_SECONDS):
         ids, pre, dec = run()
         rates.append(len(ids) / dec)
         prefill.append(len(prompt) / pre)
+    elapsed = time.perf_counter() - start
     return {
         "value": round(statistics.median(rates), 3),
         "unit": "tok/s",
         "cores": threads,
         "kind": kind,
         "sample": (f"TinyLlama-shape INT4 greedy generate, {len(prompt)}-token "
-                   f"prompt + {gen} tokens, median of 3, {threads} threads; "
-                   f"prefill {statistics.median(prefill):.3f} tok/s"),
+                   f"prompt + {gen} tokens, median of {len(rates)} runs "
+                   f"({elapsed:.1f} s), {threads} threads; prefill "
+                   f"{statistics.median(prefill):.3f} tok/s"),
     }, ids
 
 
@@ -78,6 +89,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after the timed region, copy this many MiB device "
+                         "to device (the known-size kernel that scales "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -148,12 +163,19 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES,
             "kernel": "decode loop (classifier + argmax + decode step per "
                       "token)",
             "bytes_per_launch": step_bytes,
         },
     }
+    if args.calibrate_copy_mib > 0:
+        nbytes = args.calibrate_copy_mib << 20
+        src, dst = nut.DeviceArray(nbytes), nut.DeviceArray(nbytes)
+        for _ in range(2):
+            nut.check(nut.lib().nut_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        src.close(), dst.close()
+        log(f"copied {args.calibrate_copy_mib} MiB device to device, twice")
     if not args.no_cpu:
         log("timing the CPU baseline")
         base, cpu_ids = cpu_baseline(model, prompt, gen)

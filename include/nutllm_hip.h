@@ -102,6 +102,9 @@ int nut_malloc(void **d_ptr, size_t bytes);
 int nut_free(void *d_ptr);
 int nut_memcpy_h2d(void *d_dst, const void *src, size_t bytes);
 int nut_memcpy_d2h(void *dst, const void *d_src, size_t bytes);
+/* Device-to-device copy (synchronous); also the known-size copy that
+ * calibrates HBM traffic counters. */
+int nut_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes);
 int nut_memset(void *d_dst, int value, size_t bytes);
 int nut_synchronize(void);
 

@@ -106,6 +106,7 @@ _SIGS = {
     "nut_free": (C.c_int, [_P]),
     "nut_memcpy_h2d": (C.c_int, [_P, _P, _SZ]),
     "nut_memcpy_d2h": (C.c_int, [_P, _P, _SZ]),
+    "nut_memcpy_d2d": (C.c_int, [_P, _P, _SZ]),
     "nut_memset": (C.c_int, [_P, C.c_int, _SZ]),
     "nut_synchronize": (C.c_int, []),
     "nut_qweight_create": (C.c_int, [_P, _P]),

@@ -99,6 +99,15 @@ int nut_memcpy_d2h(void *dst, const void *d_src, size_t bytes)
     });
 }
 
+int nut_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes)
+{
+    return nut::guarded([&]() {
+        nut::ensure_device();
+        nut::hip_check(hipMemcpy(d_dst, d_src, bytes, hipMemcpyDeviceToDevice),
+                       "hipMemcpy device to device");
+    });
+}
+
 int nut_memset(void *d_dst, int value, size_t bytes)
 {
     return nut::guarded([&]() {

@@ -457,7 +457,10 @@ template <class G> struct Lds {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <class G>
+// CLASSIFY: the generate loop (classifier + argmax first in every
+// iteration); otherwise the prefill loop over a.tokens_in. Two kernels, so
+// profiles tell the launches apart.
+template <class G, bool CLASSIFY>
 __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 {
     extern __shared__ float4 lds4[];
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     for (int it = 0; it < a.n_iter && !done; it++) {
         int token;
         mark(it, 0);
-        if (a.classify) {
+        if (CLASSIFY) {
             // ---------------- final rmsnorm + classifier + argmax ----
             const float *wcls = a.classifier;
             Slice<G::DIM> nw;
@@ -964,10 +967,10 @@ int device_cus()
     return cus;
 }
 
-template <class G>
-void launch(const TokenArgs &args, hipStream_t stream)
+template <class G, bool CLASSIFY>
+void launch_as(const TokenArgs &args, hipStream_t stream)
 {
-    const auto kernel = token_kernel<G>;
+    const auto kernel = token_kernel<G, CLASSIFY>;
     hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   int(Lds<G>::BYTES)),
@@ -987,6 +990,15 @@ void launch(const TokenArgs &args, hipStream_t stream)
                                          dim3(kGrid), dim3(kThreads), params,
                                          Lds<G>::BYTES, stream),
               "token kernel launch");
+}
+
+template <class G>
+void launch(const TokenArgs &args, hipStream_t stream)
+{
+    if (args.classify)
+        launch_as<G, true>(args, stream);
+    else
+        launch_as<G, false>(args, stream);
 }
 
 } // namespace
