@@ -57,11 +57,17 @@ struct Geo {
     static constexpr int ROWS_DN = cdiv(DIM, kGrid);
     // LDS staging: region 1 holds, in turn, K/V rows and the QKV, gate/up
     // and down weight rows; region 2 the Wo rows (live across attention)
-    static constexpr int KV_BYTES = 2 * KVH * NP * HD * 4;
+    // K/V staging rows padded to KROW floats (one spare 16-byte granule)
+    // so lanes reading the same column of consecutive rows hit distinct
+    // LDS banks
+    static constexpr int KROW = HD + 4;
+    static constexpr int KV_BYTES = 2 * KVH * NP * KROW * 4;
     static constexpr int W_QKV = ROWS_QKV * (RB_DIM + SB_DIM);
     static constexpr int W_GU = ROWS_GU * (RB_DIM + SB_DIM);
     static constexpr int W_DN = ROWS_DN * (RB_FFN + SB_FFN);
     static constexpr int W_WO = ROWS_WO * (RB_DIM + SB_DIM);
+    // region 1 holds, in turn, the K/V staging (packed by the live position
+    // count) and the QKV, gate/up and W2 rows of a phase
     static constexpr int R1 = cmax(cmax(KV_BYTES, W_QKV), cmax(W_GU, W_DN));
     static constexpr int R2 = W_WO;
     // weight arena layout of one layer
@@ -70,7 +76,8 @@ struct Geo {
     static_assert(RB_FFN % 16 == 0 && SB_FFN % 16 == 0 && SB_DIM % 16 == 0,
                   "16-byte DMA granules");
     static_assert(HEADS % kWaves == 0, "heads split over waves");
-    static_assert(HD % 4 == 0 && kWave % (HD / 4) == 0, "head_dim");
+    static_assert(HD == 64 && HPW * (HD / 4) == kWave && GROUP % HPW == 0,
+                  "attention: 16 lanes per head row, a wave's heads share a kv head");
     static_assert((DIM + 2 * KVD) % 2 == 0 && KVD % 2 == 0, "row pairs");
 };
 
@@ -160,6 +167,26 @@ __device__ __forceinline__ void dma_wait()
 {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+}
+
+// Rows [0, n) of 64-float rows at src into LDS rows of 68 floats (16 data
+// granules + 1 spare): LDS granule j holds row j / 17, granule j % 17.
+__device__ __forceinline__ void dma_padded_rows(float *lds_dst,
+                                                const float *src, int n)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int instrs = (n * 17 + kWave - 1) / kWave;
+    for (int i = wave_index(); i < instrs; i += kWaves) {
+        const int j = i * kWave + lane;
+        const int row = j / 17, g = j - row * 17;
+        if (row < n && g < 16)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(
+                    src + row * 64 + g * 4),
+                (__attribute__((address_space(3))) void *)(
+                    reinterpret_cast<char *>(lds_dst) + i * 1024),
+                16, 0, 0);
+    }
 }
 
 // --------------------------------------------------------- x staging --
@@ -470,8 +497,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     float *qkv = lds + L::QKV, *scores = lds + L::SCORES, *red = lds + L::RED;
     uint8_t *r1 = reinterpret_cast<uint8_t *>(lds + L::R1);
     uint8_t *r2 = reinterpret_cast<uint8_t *>(lds + L::R2);
-    float *kst = lds + L::R1;                       // [KVH][NP][HD]
-    float *vst = kst + G::KVH * G::NP * G::HD;
+    // K/V staging of an n-position step: K [KVH][n][KROW], then V
+    float *kst = lds + L::R1;
     int *misc = reinterpret_cast<int *>(lds + L::MISC);
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -552,6 +579,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     int count = 0, done = 0, last_token = 0;
     // Tag of the hidden state the next classifier reads; 0 = hidden_in.
     unsigned hidden_tag = 0;
+    // Each phase's weight rows (and attention's K/V rows) are issued just
+    // before the wait for its input. Measured: issuing them a phase earlier
+    // puts the bulk reads inside other workgroups' exchange waits or under
+    // a compute phase, and both slow the token down.
 
     for (int it = 0; it < a.n_iter && !done; it++) {
         int token;
@@ -762,15 +793,17 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 }
             }
             tag++;
-            // K/V rows of earlier positions and the Wo rows stream into LDS
-            // while the q/k/v exchange completes.
+            // K/V rows of earlier positions stream into LDS while the q/k/v
+            // exchange completes.
             __syncthreads();
+            const int n = pos + 1;
+            float *vst = kst + G::KVH * n * G::KROW;
             if (pos > 0)
                 for (int kvh = 0; kvh < G::KVH; kvh++) {
-                    dma(kst + kvh * G::NP * G::HD, kc + size_t(kvh) * a.max_seq * G::HD,
-                        pos * G::HD * 4);
-                    dma(vst + kvh * G::NP * G::HD, vc + size_t(kvh) * a.max_seq * G::HD,
-                        pos * G::HD * 4);
+                    dma_padded_rows(kst + kvh * n * G::KROW,
+                                    kc + size_t(kvh) * a.max_seq * G::HD, pos);
+                    dma_padded_rows(vst + kvh * n * G::KROW,
+                                    vc + size_t(kvh) * a.max_seq * G::HD, pos);
                 }
             stage_wo(l);
             mark(it, 3 + 9 * l);
@@ -783,82 +816,83 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 const int which = i >= G::KVD;
                 const int j = i - which * G::KVD;
                 const int kvh = j / G::HD, d = j - kvh * G::HD;
-                (which ? vst : kst)[(kvh * G::NP + pos) * G::HD + d] = qkv[G::DIM + i];
+                (which ? vst : kst)[(kvh * n + pos) * G::KROW + d] = qkv[G::DIM + i];
             }
+
             __syncthreads();
             mark(it, 4 + 9 * l);
             {
-                const int n = pos + 1;
-                constexpr int Q4 = G::HD / 4;   // float4 per K/V row
-                constexpr int PG = kWave / Q4;  // positions per wave pass
-                const int d4 = lane % Q4, pg = lane / Q4;
-                float *sc = scores + wave * G::HPW * G::NP;
-                const int head0 = wave * G::HPW;
-                // scores: Q4 lanes per position, reduced by shuffles
-                for (int p0 = 0; p0 < n; p0 += PG) {
-                    const int p = p0 + pg;
+                // Wave w: query heads 4w..4w+3, all of kv head 4w / GROUP.
+                // Lane (hh = lane / 16, r = lane % 16): scores of head hh at
+                // positions r, r + 16, ...; then context quad r of head hh.
+                constexpr int PASSES = cdiv(G::NP, 16);
+                const int hh = lane >> 4, r = lane & 15;
+                const int head = wave * G::HPW + hh;
+                const int g = (wave * G::HPW) / G::GROUP;
+                const float *kg = kst + g * n * G::KROW;
+                const float *vg = vst + g * n * G::KROW;
+                const float4 *q4 = reinterpret_cast<const float4 *>(qkv + head * G::HD);
+                float *sc = scores + head * G::NP;
+                float s[PASSES];
+                float m = -INFINITY;
 #pragma unroll
-                    for (int hh = 0; hh < G::HPW; hh++) {
-                        const int kvh = (head0 + hh) / G::GROUP;
-                        float part = 0.0f;
+                for (int ps = 0; ps < PASSES; ps++) {
+                    s[ps] = -INFINITY;
+                    if (ps * 16 < n) {
+                        const int p = ps * 16 + r;
                         if (p < n) {
-                            const float4 k = reinterpret_cast<const float4 *>(
-                                kst + (kvh * G::NP + p) * G::HD)[d4];
-                            const float4 q = reinterpret_cast<const float4 *>(
-                                qkv + (head0 + hh) * G::HD)[d4];
-                            part = fmaf(q.x, k.x, fmaf(q.y, k.y, fmaf(q.z, k.z, q.w * k.w)));
+                            const float4 *k4 =
+                                reinterpret_cast<const float4 *>(kg + p * G::KROW);
+                            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                            for (int d4 = 0; d4 < 16; d4 += 2) {
+                                const float4 k0 = k4[d4], q0 = q4[d4];
+                                const float4 k1 = k4[d4 + 1], q1 = q4[d4 + 1];
+                                a0 = fmaf(q0.x, k0.x, a0);
+                                a1 = fmaf(q1.x, k1.x, a1);
+                                a0 = fmaf(q0.y, k0.y, a0);
+                                a1 = fmaf(q1.y, k1.y, a1);
+                                a0 = fmaf(q0.z, k0.z, a0);
+                                a1 = fmaf(q1.z, k1.z, a1);
+                                a0 = fmaf(q0.w, k0.w, a0);
+                                a1 = fmaf(q1.w, k1.w, a1);
+                            }
+                            s[ps] = (a0 + a1) * a.attn_scale;
                         }
-                        static_assert(Q4 == 16, "one DPP row per position");
-                        part = row16_sum(part);
-                        if (p < n && d4 == 0)
-                            sc[hh * G::NP + p] = part * a.attn_scale;
+                        m = fmaxf(m, s[ps]);
                     }
                 }
-                // softmax per head (wave-local scores)
-                float total[G::HPW];
+                m = row16_max(m);
+                float total = 0.0f;
 #pragma unroll
-                for (int hh = 0; hh < G::HPW; hh++) {
-                    float m = -INFINITY;
-                    for (int p = lane; p < n; p += kWave)
-                        m = fmaxf(m, sc[hh * G::NP + p]);
-                    m = wave_maximum(m);
-                    float s = 0.0f;
-                    for (int p = lane; p < n; p += kWave) {
-                        const float e = expf(sc[hh * G::NP + p] - m);
-                        sc[hh * G::NP + p] = e;
-                        s += e;
+                for (int ps = 0; ps < PASSES; ps++) {
+                    if (ps * 16 < n) {
+                        const int p = ps * 16 + r;
+                        if (p < n) {
+                            const float e = expf(s[ps] - m);
+                            sc[p] = e;
+                            total += e;
+                        }
                     }
-                    total[hh] = wave_total(s);
                 }
-                // context: lane <-> (quad d4 of the row, head hh of the wave)
-                {
-                    static_assert(G::HPW * Q4 == kWave, "one DPP row per head");
-                    const int hh = lane / Q4;
-                    const int kvh = (head0 + hh) / G::GROUP;
-                    const float4 *vcol = reinterpret_cast<const float4 *>(
-                        vst + kvh * G::NP * G::HD) + d4;
-                    const float *w = sc + hh * G::NP;
-                    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    for (int p = 0; p < n; p++) {
-                        const float4 v = vcol[p * Q4];
-                        const float wgt = w[p];
-                        acc.x = fmaf(wgt, v.x, acc.x);
-                        acc.y = fmaf(wgt, v.y, acc.y);
-                        acc.z = fmaf(wgt, v.z, acc.z);
-                        acc.w = fmaf(wgt, v.w, acc.w);
-                    }
-                    float tot = total[0];
-#pragma unroll
-                    for (int h = 1; h < G::HPW; h++)
-                        if (hh == h)
-                            tot = total[h];
-                    const float inv = 1.0f / tot;
-                    const int e0 = (head0 + hh) * G::HD + 4 * d4;
-                    xs[swz(e0)] = acc.x * inv;
-                    xs[swz(e0 + 1)] = acc.y * inv;
-                    xs[swz(e0 + 2)] = acc.z * inv;
-                    xs[swz(e0 + 3)] = acc.w * inv;
+                total = row16_sum(total);
+                // context: lanes of head hh own quad r of its output row
+                const float4 *v4 = reinterpret_cast<const float4 *>(vg) + r;
+                float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int p = 0; p < n; p++) {
+                    const float4 v = v4[p * (G::KROW / 4)];
+                    const float w = sc[p];
+                    acc.x = fmaf(w, v.x, acc.x);
+                    acc.y = fmaf(w, v.y, acc.y);
+                    acc.z = fmaf(w, v.z, acc.z);
+                    acc.w = fmaf(w, v.w, acc.w);
                 }
+                const float inv = 1.0f / total;
+                const int e0 = head * G::HD + 4 * r;
+                xs[swz(e0)] = acc.x * inv;
+                xs[swz(e0 + 1)] = acc.y * inv;
+                xs[swz(e0 + 2)] = acc.z * inv;
+                xs[swz(e0 + 3)] = acc.w * inv;
             }
             __syncthreads();
             block_sums(xs, xsum, G::DIM);
