@@ -129,17 +129,28 @@ __device__ __forceinline__ float ubyte1(uint32_t v) { return float((v >> 8) & 0x
 __device__ __forceinline__ float ubyte2(uint32_t v) { return float((v >> 16) & 0xffu); }
 __device__ __forceinline__ float ubyte3(uint32_t v) { return float(v >> 24); }
 
+// Keeps v opaque to known-bits folding, so byte conversions of a masked
+// word stay single v_cvt_f32_ubyte{0..3} instead of a bit-field extract
+// per nibble. Emits no instruction.
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // sum_k u_k x[k] over one INT4 chunk (32 weights, offset-binary codes).
 // Byte b of word j holds weights 8j+2b (low nibble) and 8j+2b+1 (high).
+// High nibbles are converted in place (16 u) and their accumulator scaled
+// by 1/16 once; power-of-two scaling commutes with rounding, so the result
+// equals accumulating u x.
 __device__ __forceinline__ float dot_int4_chunk(uint4 w, const float *x)
 {
-    const uint32_t words[4] = {w.x ^ 0x88888888u, w.y ^ 0x88888888u,
-                               w.z ^ 0x88888888u, w.w ^ 0x88888888u};
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const uint32_t lo = words[j] & 0x0f0f0f0fu;
-        const uint32_t hi = (words[j] >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo = opaque((words[j] ^ 0x88888888u) & 0x0f0f0f0fu);
+        const uint32_t hi = opaque((words[j] ^ 0x88888888u) & 0xf0f0f0f0u);
         const float *xs = x + 8 * j;
         a0 = fmaf(ubyte0(lo), xs[0], a0);
         a1 = fmaf(ubyte0(hi), xs[1], a1);
@@ -150,7 +161,7 @@ __device__ __forceinline__ float dot_int4_chunk(uint4 w, const float *x)
         a0 = fmaf(ubyte3(lo), xs[6], a0);
         a1 = fmaf(ubyte3(hi), xs[7], a1);
     }
-    return a0 + a1;
+    return fmaf(a1, 0.0625f, a0);
 }
 
 // sum_k u_k x[k] over one INT8 chunk (16 weights, offset-binary codes).

@@ -340,16 +340,19 @@ __device__ float take(const uint64_t *src, float *dst, unsigned tag,
 
 // ------------------------------------------------------ quantised rows --
 
+// sum_k u_k x_k over one INT4 block (u = q + 8, offset binary). The high
+// nibbles are converted in place (16 u), and their accumulator is scaled by
+// 1/16 once: power-of-two scaling commutes with rounding, so the result is
+// the same as accumulating u x.
 __device__ __forceinline__ float dot_block_int4(const uint4 &w,
                                                 const float4 (&x)[8])
 {
-    const uint32_t words[4] = {w.x ^ 0x88888888u, w.y ^ 0x88888888u,
-                               w.z ^ 0x88888888u, w.w ^ 0x88888888u};
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const uint32_t lo = words[j] & 0x0f0f0f0fu;
-        const uint32_t hi = (words[j] >> 4) & 0x0f0f0f0fu;
+        const uint32_t lo = opaque((words[j] ^ 0x88888888u) & 0x0f0f0f0fu);
+        const uint32_t hi = opaque((words[j] ^ 0x88888888u) & 0xf0f0f0f0u);
         const float4 xa = x[2 * j], xb = x[2 * j + 1];
         a0 = fmaf(ubyte0(lo), xa.x, a0);
         a1 = fmaf(ubyte0(hi), xa.y, a1);
@@ -360,7 +363,7 @@ __device__ __forceinline__ float dot_block_int4(const uint4 &w,
         a0 = fmaf(ubyte3(lo), xb.z, a0);
         a1 = fmaf(ubyte3(hi), xb.w, a1);
     }
-    return a0 + a1;
+    return fmaf(a1, 0.0625f, a0);
 }
 
 __device__ __forceinline__ float dot_block_int8(const uint4 &w0,
