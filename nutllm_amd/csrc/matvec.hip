@@ -1,9 +1,14 @@
 // matvec.hip — standalone quantised and fp32 matvec kernels for gfx950.
 //
-// Bandwidth-bound, no MFMA: each wave streams whole rows with 128-bit
-// loads (lane l reads bytes [16l, 16l+16) of every 1 KB stretch of a row),
-// dequantises in registers and reduces across the wave. x is staged once
-// per workgroup in LDS with its per-chunk sums.
+// Bandwidth-bound, no MFMA. Fast layout (block 32, cols % 32 == 0): a wave
+// owns R consecutive rows; lane l handles 16-byte chunks l, l + 64, ... of
+// each row (one INT4 block or half an INT8 block per chunk). Every lane
+// issues its R row chunks (non-temporal: streamed once) and its x chunk
+// together, sums the x chunk in registers for the offset-binary bias, and
+// the R row sums are reduced with DPP at the end. No LDS, no barrier: the
+// whole matrix is in flight after one round of issue.
+// Other layouts (blocks straddling rows, other block sizes) run one row
+// per wave from an LDS copy of x.
 #include "kernels.hpp"
 #include "runtime.hpp"
 
@@ -13,38 +18,93 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kRows = 2; // rows per wave tile
 
-__global__ __launch_bounds__(kThreads) void matvec_q_kernel(QMat m,
-                                                            const float *x,
-                                                            float *y)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 load_stream(const uint8_t *p)
 {
-    extern __shared__ float lds[];
-    const int cw = chunk_weights(m.type);
-    float *xs = lds;
-    float *xsum = lds + m.cols;
-    stage_x(x, xs, xsum, m.cols, cw);
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int QT, int R>
+__global__ __launch_bounds__(kThreads) void matvec_q_fast(QMat m,
+                                                          const float *__restrict__ x,
+                                                          float *__restrict__ y)
+{
+    constexpr int CW = QT == 1 ? 32 : 16; // weights per 16-byte chunk
+    constexpr float kBias = QT == 1 ? 8.0f : 128.0f;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row0 = (blockIdx.x * kWaves + threadIdx.x / kWave) * R;
+    if (row0 >= m.rows)
+        return; // wave-uniform
+    const int row_bytes = QT == 1 ? m.cols / 2 : m.cols;
+    const int chunks = row_bytes / 16;
+    const int blocks_per_row = m.cols / 32;
+    const uint8_t *rows[R];
+    const uint16_t *scales[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int rr = min(row0 + r, m.rows - 1); // tail rows re-read the last
+        rows[r] = m.data + size_t(rr) * row_bytes;
+        scales[r] = m.scales + size_t(rr) * blocks_per_row;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        acc[r] = 0.0f;
+    for (int c = lane; c < chunks; c += kWave) {
+        const int block = QT == 1 ? c : (c >> 1);
+        uint4 w[R];
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w[r] = load_stream(rows[r] + 16 * c);
+            s[r] = half_bits_to_float(scales[r][block]);
+        }
+        float xc[CW];
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + c * CW);
+#pragma unroll
+        for (int q = 0; q < CW / 4; q++) {
+            const float4 v = x4[q];
+            xc[4 * q] = v.x;
+            xc[4 * q + 1] = v.y;
+            xc[4 * q + 2] = v.z;
+            xc[4 * q + 3] = v.w;
+        }
+        float xsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CW; i++)
+            xsum += xc[i];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float d = QT == 1 ? dot_int4_chunk(w[r], xc) : dot_int8_chunk(w[r], xc);
+            acc[r] = fmaf(s[r], d - kBias * xsum, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = wave_total(acc[r]);
+        if (lane == 0 && row0 + r < m.rows)
+            y[row0 + r] = v;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void matvec_q_generic(QMat m,
+                                                             const float *x,
+                                                             float *y)
+{
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < m.cols; i += blockDim.x)
+        xs[i] = x[i];
+    __syncthreads();
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    if (fast_layout(m)) {
-        const int tiles = (m.rows + kRows - 1) / kRows;
-        for (int t = blockIdx.x * kWaves + wave; t < tiles;
-             t += gridDim.x * kWaves) {
-            const int row0 = t * kRows;
-            float out[kRows];
-            qrows_fast<kRows>(m, row0, xs, xsum, out);
-#pragma unroll
-            for (int r = 0; r < kRows; r++)
-                if (lane == r && row0 + r < m.rows)
-                    y[row0 + r] = out[r];
-        }
-    } else {
-        for (int row = blockIdx.x * kWaves + wave; row < m.rows;
-             row += gridDim.x * kWaves) {
-            const float v = qrow_generic(m, row, xs);
-            if (lane == 0)
-                y[row] = v;
-        }
+    for (int row = blockIdx.x * kWaves + wave; row < m.rows;
+         row += gridDim.x * kWaves) {
+        const float v = qrow_generic(m, row, xs);
+        if (lane == 0)
+            y[row] = v;
     }
 }
 
@@ -89,21 +149,44 @@ int grid_for(int work_items)
 
 } // namespace
 
+// LDS of a kernel that stages x and its per-chunk sums (the step kernels).
 size_t matvec_q_lds_bytes(const QMat &m)
 {
     const int cw = chunk_weights(m.type);
     return sizeof(float) * (size_t(m.cols) + (m.cols + cw - 1) / cw);
 }
 
+template <int QT, int R>
+void launch_fast(const QMat &m, const float *x, float *y, hipStream_t stream)
+{
+    const int waves = (m.rows + R - 1) / R;
+    const int blocks = (waves + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL((matvec_q_fast<QT, R>), dim3(blocks), dim3(kThreads), 0,
+                       stream, m, x, y);
+}
+
 void launch_matvec_q(const QMat &m, const float *x, float *y,
                      hipStream_t stream)
 {
-    const size_t lds = matvec_q_lds_bytes(m);
-    require(lds <= 64 * 1024, NUT_EINVAL,
-            "quantized matvec: input dimension exceeds LDS staging");
-    const int work = fast_layout(m) ? (m.rows + kRows - 1) / kRows : m.rows;
-    hipLaunchKernelGGL(matvec_q_kernel, dim3(grid_for(work)), dim3(kThreads),
-                       lds, stream, m, x, y);
+    if (fast_layout(m)) {
+        // rows per wave: enough waves to fill 256 CUs, as many rows in
+        // flight per wave as that allows
+        const int r = m.rows >= 4096 ? 4 : m.rows >= 1024 ? 2 : 1;
+        if (m.type == 1)
+            r == 4 ? launch_fast<1, 4>(m, x, y, stream)
+                   : r == 2 ? launch_fast<1, 2>(m, x, y, stream)
+                            : launch_fast<1, 1>(m, x, y, stream);
+        else
+            r == 4 ? launch_fast<0, 4>(m, x, y, stream)
+                   : r == 2 ? launch_fast<0, 2>(m, x, y, stream)
+                            : launch_fast<0, 1>(m, x, y, stream);
+    } else {
+        const size_t lds = sizeof(float) * size_t(m.cols);
+        require(lds <= 64 * 1024, NUT_EINVAL,
+                "quantized matvec: input dimension exceeds LDS staging");
+        hipLaunchKernelGGL(matvec_q_generic, dim3(grid_for(m.rows)), dim3(kThreads),
+                           lds, stream, m, x, y);
+    }
     check_launch("quantized matvec");
 }
 
