@@ -92,6 +92,18 @@ void launch_classifier(const DecodeShape &s, const float *hidden,
 void launch_pick_token(const DecodeShape &s, const float *part_val,
                        const int *part_idx, int parts, StepState *state,
                        int *tokens, hipStream_t stream);
+// Fast step kernels (step.hip): layers whose matrices all use 32-wide
+// blocks along whole rows, head_dim 64 or 128.
+struct StepBuffers {
+    float *hidden, *query, *context, *act, *xn, *attn_part;
+};
+bool step_fast_supported(const DecodeShape &s, const LayerView &w);
+size_t step_attn_part_floats(const DecodeShape &s);
+void launch_layer_fast(const DecodeShape &s, const LayerView &w,
+                       const float2 *rope, const int *length, float *k_layer,
+                       float *v_layer, const StepBuffers &b,
+                       const StepState *state, hipStream_t stream);
+
 // Tiny state writers, enqueued on the stream (graph-safe, no memset).
 void launch_set_int(int *target, int value, hipStream_t stream);
 void launch_reset_state(StepState *state, int token, hipStream_t stream);

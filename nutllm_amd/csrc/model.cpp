@@ -4,6 +4,7 @@
 // (src/quant_model.cpp:161-172,212-213; src/generate.cpp:177-181).
 #include "model.hpp"
 #include "persistent.hpp"
+#include "prefill.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -72,6 +73,15 @@ void check_ready(const nut_model &m, const char *who)
             fail(NUT_EINVAL, std::string(who) + ": layer count mismatch");
 }
 
+// True when every layer can run the fast step kernels.
+bool fast_steps(const nut_model &m)
+{
+    for (const DeviceLayer &l : m.layers)
+        if (!step_fast_supported(m.shape, l.view))
+            return false;
+    return true;
+}
+
 // Enqueue one decode step reading its token from token_ptr (device).
 void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
 {
@@ -80,6 +90,23 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
     launch_embed(s, m.embeddings.as<float>(), token_ptr, state,
                  m.hidden.as<float>(), m.stream);
     const size_t layer_elems = kv.layer_elements();
+    if (fast_steps(m)) {
+        if (m.xn.get() == nullptr) {
+            m.xn.allocate(std::max(s.dim, s.ffn_dim) * sizeof(float));
+            m.attn_part.allocate(step_attn_part_floats(s) * sizeof(float));
+        }
+        const StepBuffers b{m.hidden.as<float>(), m.query.as<float>(),
+                            m.context.as<float>(), m.act.as<float>(),
+                            m.xn.as<float>(), m.attn_part.as<float>()};
+        for (size_t l = 0; l < m.layers.size(); l++)
+            launch_layer_fast(s, m.layers[l].view, m.rope.as<float2>(),
+                              kv.device_length.as<int>(),
+                              kv.keys.as<float>() + l * layer_elems,
+                              kv.values.as<float>() + l * layer_elems, b, state,
+                              m.stream);
+        launch_finish_step(state, kv.device_length.as<int>(), m.stream);
+        return;
+    }
     for (size_t l = 0; l < m.layers.size(); l++)
         launch_layer(s, m.layers[l].view, m.rope.as<float2>(),
                      kv.device_length.as<int>(),
@@ -92,6 +119,71 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
 }
 
 void sync(nut_model &m) { hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize"); }
+
+// Prompts of at least this many tokens run as a batch (GEMM prefill).
+constexpr size_t kPrefillGemmMin = 16;
+
+// The batched prefill applies when every layer uses 32-wide blocks, the
+// head size matches its attention tiles, and per-token steps are not
+// forced.
+bool use_prefill_gemm(const nut_model &m, size_t count)
+{
+    if (m.path == 1 || count < kPrefillGemmMin)
+        return false;
+    for (const DeviceLayer &l : m.layers)
+        if (!prefill_gemm_supported(m.shape, l.view))
+            return false;
+    return true;
+}
+
+// Tokens [0, count) (device ids in m.prompt) through every layer as a batch
+// at positions 0 .. count - 1; K/V rows land in the cache and the last
+// token's hidden state in m.hidden.
+void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
+{
+    const nut_config &c = m.config;
+    const DecodeShape &s = m.shape;
+    const size_t kvd = kv_heads_of(c) * c.head_dim;
+    if (m.pf_h.get() == nullptr) {
+        const size_t rows = c.max_seq;
+        m.pf_h.allocate(rows * c.dim * sizeof(float));
+        m.pf_x.allocate(rows * std::max(c.dim, c.ffn_dim) * sizeof(float));
+        m.pf_q.allocate(rows * c.dim * sizeof(float));
+        m.pf_k.allocate(rows * kvd * sizeof(float));
+        m.pf_v.allocate(rows * kvd * sizeof(float));
+        m.pf_ctx.allocate(rows * c.dim * sizeof(float));
+        m.pf_g.allocate(rows * c.ffn_dim * sizeof(float));
+        m.pf_u.allocate(rows * c.ffn_dim * sizeof(float));
+    }
+    const int t = int(count);
+    float *h = m.pf_h.as<float>(), *x = m.pf_x.as<float>();
+    float *q = m.pf_q.as<float>(), *k = m.pf_k.as<float>(), *v = m.pf_v.as<float>();
+    float *ctx = m.pf_ctx.as<float>(), *g = m.pf_g.as<float>(), *u = m.pf_u.as<float>();
+    launch_embed_rows(m.embeddings.as<float>(), m.prompt.as<int>(), h, t, s.dim,
+                      m.stream);
+    const size_t layer_elems = kv.layer_elements();
+    for (size_t l = 0; l < m.layers.size(); l++) {
+        const LayerView &w = m.layers[l].view;
+        float *kc = kv.keys.as<float>() + l * layer_elems;
+        float *vc = kv.values.as<float>() + l * layer_elems;
+        launch_rmsnorm_rows(h, w.attention_norm, x, t, s.dim, m.stream);
+        launch_qgemm_rows(x, t, w.query, q, s.dim, false, m.stream);
+        launch_qgemm_rows(x, t, w.key, k, int(kvd), false, m.stream);
+        launch_qgemm_rows(x, t, w.value, v, int(kvd), false, m.stream);
+        launch_rope_store(q, k, v, m.rope.as<float2>(), kc, vc, s, t, 0, m.stream);
+        launch_attention_prefill(q, kc, vc, ctx, s, t, 0, m.stream);
+        launch_qgemm_rows(ctx, t, w.output, h, s.dim, true, m.stream);
+        launch_rmsnorm_rows(h, w.ffn_norm, x, t, s.dim, m.stream);
+        launch_qgemm_rows(x, t, w.gate, g, s.ffn_dim, false, m.stream);
+        launch_qgemm_rows(x, t, w.up, u, s.ffn_dim, false, m.stream);
+        launch_silu_mul(g, u, x, size_t(t) * s.ffn_dim, m.stream);
+        launch_qgemm_rows(x, t, w.down, h, s.dim, true, m.stream);
+    }
+    hip_check(hipMemcpyAsync(m.hidden.get(), h + size_t(t - 1) * s.dim,
+                             s.dim * sizeof(float), hipMemcpyDeviceToDevice,
+                             m.stream),
+              "hipMemcpyAsync");
+}
 
 double now() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
 
@@ -427,7 +519,9 @@ void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
         hip_check(hipMemcpyAsync(m.prompt.get(), tokens, valid * sizeof(int),
                                  hipMemcpyHostToDevice, m.stream),
                   "hipMemcpyAsync");
-        if (use_token_kernel(m, valid)) {
+        if (use_prefill_gemm(m, valid)) {
+            prefill_batch(m, kv, valid);
+        } else if (use_token_kernel(m, valid)) {
             run_token_kernel(m, kv, 0, valid, false, m.prompt.as<int>(), nullptr,
                              m.hidden.as<float>());
         } else {
@@ -440,9 +534,12 @@ void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
             hip_check(hipMemcpyAsync(hidden, m.hidden.get(), m.config.dim * sizeof(float),
                                      hipMemcpyDeviceToHost, m.stream),
                       "hipMemcpyAsync");
+        kv.length = valid;
+        // the step kernels read the length from the device; the batched and
+        // token-kernel paths do not advance it themselves
+        kv.sync_length(m.stream);
         sync(m);
         check_token_error(m);
-        kv.length = valid;
     }
     require(valid == count, NUT_EOUTOFRANGE, "quantized decode: token out of range");
 }

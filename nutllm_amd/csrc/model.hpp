@@ -58,12 +58,15 @@ struct nut_model {
 
     // Step workspace.
     nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
+    nut::DeviceBuffer xn, attn_part; // fast step kernels
     nut::DeviceBuffer part_val, part_idx, state, tokens, prompt;
     hipStream_t stream = nullptr;
     hipEvent_t decode_begin = nullptr, decode_end = nullptr;
     // Cooperative token kernel state.
     int path = 0; // 0 auto, 1 step kernels, 2 token kernel
     nut::DeviceBuffer exchange, token_error, timeline;
+    // Prefill GEMM path: activations of a whole prompt, max_seq rows each.
+    nut::DeviceBuffer pf_h, pf_x, pf_q, pf_k, pf_v, pf_ctx, pf_g, pf_u;
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
     int timeline_wgs = 0;        // workgroups it covers
     unsigned launch_count = 0;

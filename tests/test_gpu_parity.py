@@ -289,3 +289,41 @@ def test_tiny_matches_reference_golden(gpu, qtype, tag):
     logits = dev.logits(g["hidden"][len(g["prompt"]) - 1])
     assert rel_l2(logits, g["logits"]) <= TOL
     dev.close()
+
+
+PREFILL_TOL = 2e-3  # rel-L2, batched (GEMM) prefill
+
+
+@pytest.mark.parametrize("prompt_len", [40, 130])
+def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
+    """Prompts of 16+ tokens run as a batch (MFMA GEMMs, causal attention).
+    Hidden state and K/V rows within rel-L2 2e-3 of the per-token path
+    (oracle for 40 tokens, the device step kernels for 130), and the greedy
+    ids that follow the prefill identical to the oracle's."""
+    model, _, _, dev = tinyllama_int4
+    prompt = gpu.synth_tokens(11, model.config.vocab_size, prompt_len)
+    cache = gpu.KVCache(model.config)
+    h = dev.prefill(cache, prompt)
+    if prompt_len <= 40:
+        om = O.oracle_model(model)
+        ref = om.prefill(prompt)
+        kv_ref = lambda l, kvh, p: om.kv_row(l, kvh, p)  # noqa: E731
+    else:
+        dev.set_path(1)
+        ref_cache = gpu.KVCache(model.config)
+        ref = dev.prefill(ref_cache, prompt)
+        dev.set_path(0)
+        kv_ref = lambda l, kvh, p: ref_cache.key_value(l, kvh, p)  # noqa: E731
+    err = rel_l2(h, ref)
+    print(f"prefill {prompt_len} tokens: hidden rel-L2 {err:.2e}", flush=True)
+    assert err <= PREFILL_TOL
+    for layer in (0, model.config.layers - 1):
+        for kvh in range(model.config.kv_heads):
+            for p in (0, prompt_len // 2, prompt_len - 1):
+                k, v = cache.key_value(layer, kvh, p)
+                rk, rv = kv_ref(layer, kvh, p)
+                assert rel_l2(k, rk) <= PREFILL_TOL and rel_l2(v, rv) <= PREFILL_TOL
+    if prompt_len <= 40:
+        ids, _ = dev.generate(prompt, 8)
+        ref_ids, _, _ = om.generate(prompt, 8)
+        assert ids == ref_ids
