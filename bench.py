@@ -89,6 +89,8 @@ def long_prompt(args, nut, workloads):
     log(f"built synthetic model in {time.time() - t:.1f}s")
     dev = model.to_device()
     cfg = model.config
+    if args.path == "steps":
+        dev.set_path(nut.PATH_STEPS)
     for _ in range(args.warmup):
         dev.generate(prompt, gen)
     pre, dec, toks, dms = [], [], 0, []
@@ -130,6 +132,10 @@ def main():
                     help="tinyllama_int4 (default): the headline line below; "
                          "the others print one line of prefill and decode "
                          "tok/s for the long-prompt configurations")
+    ap.add_argument("--path", default="auto", choices=["auto", "steps"],
+                    help="steps: eager per-token step kernels only (no token "
+                         "kernel, batched prefill or graph replay), for "
+                         "profiling the step kernels")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the timed region, copy this many MiB device "
                          "to device (the known-size kernel that scales "

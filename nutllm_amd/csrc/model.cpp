@@ -82,6 +82,25 @@ bool fast_steps(const nut_model &m)
     return true;
 }
 
+// The captured iteration names the model's buffers; weight uploads drop it.
+void drop_graph(nut_model &m)
+{
+    if (m.step_graph != nullptr) {
+        hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize");
+        (void)hipGraphExecDestroy(m.step_graph);
+        m.step_graph = nullptr;
+    }
+}
+
+// Workspace of the fast step kernels (allocated before any capture).
+void prepare_fast_steps(nut_model &m)
+{
+    if (m.xn.get() == nullptr) {
+        m.xn.allocate(std::max(m.shape.dim, m.shape.ffn_dim) * sizeof(float));
+        m.attn_part.allocate(step_attn_part_floats(m.shape) * sizeof(float));
+    }
+}
+
 // Enqueue one decode step reading its token from token_ptr (device).
 void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
 {
@@ -91,10 +110,7 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
                  m.hidden.as<float>(), m.stream);
     const size_t layer_elems = kv.layer_elements();
     if (fast_steps(m)) {
-        if (m.xn.get() == nullptr) {
-            m.xn.allocate(std::max(s.dim, s.ffn_dim) * sizeof(float));
-            m.attn_part.allocate(step_attn_part_floats(s) * sizeof(float));
-        }
+        prepare_fast_steps(m);
         const StepBuffers b{m.hidden.as<float>(), m.query.as<float>(),
                             m.context.as<float>(), m.act.as<float>(),
                             m.xn.as<float>(), m.attn_part.as<float>()};
@@ -247,6 +263,7 @@ nut_model *create_model(const nut_config &config, int type, bool tied)
 void set_globals(nut_model &m, const float *embeddings,
                  const float *final_norm, const float *lm_head)
 {
+    drop_graph(m);
     const size_t dim = m.config.dim, vocab = m.config.vocab_size;
     require(embeddings != nullptr && final_norm != nullptr &&
                 (m.tied || lm_head != nullptr),
@@ -261,6 +278,7 @@ void set_globals(nut_model &m, const float *embeddings,
 void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
                const float *attention_norm, const float *ffn_norm)
 {
+    drop_graph(m);
     const nut_config &c = m.config;
     require(layer < c.layers, NUT_EOUTOFRANGE, "quantized model: layer out of range");
     require(attention_norm != nullptr && ffn_norm != nullptr, NUT_EINVAL,
@@ -375,6 +393,8 @@ void nut_kvcache::sync_length(hipStream_t stream)
 
 nut_model::~nut_model()
 {
+    if (step_graph != nullptr)
+        (void)hipGraphExecDestroy(step_graph);
     if (decode_begin != nullptr)
         (void)hipEventDestroy(decode_begin);
     if (decode_end != nullptr)
@@ -589,13 +609,37 @@ void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
         run_token_kernel(m, kv, prompt_len, steps, true, nullptr, m.hidden.as<float>(),
                          m.scratch_hidden.as<float>());
     } else {
-        for (size_t i = 0; i < steps; i++) {
+        auto iteration = [&]() {
             launch_classifier(m.shape, m.hidden.as<float>(), m.final_norm.as<float>(),
                               m.output_weights(), nullptr, m.part_val.as<float>(),
                               m.part_idx.as<int>(), state, m.stream);
             launch_pick_token(m.shape, m.part_val.as<float>(), m.part_idx.as<int>(),
                               parts, state, m.tokens.as<int>(), m.stream);
             enqueue_step(m, kv, &state->token);
+        };
+        if (m.path == 1 || steps < 2) {
+            for (size_t i = 0; i < steps; i++)
+                iteration();
+        } else {
+            // Every kernel of an iteration reads its token, position and
+            // stop flag from device memory, so one captured iteration is
+            // replayed for every token; the cache and buffers it names are
+            // the model's own (the generation cache lives as long as it).
+            if (m.step_graph == nullptr) {
+                if (fast_steps(m))
+                    prepare_fast_steps(m);
+                hipGraph_t graph = nullptr;
+                hip_check(hipStreamBeginCapture(m.stream, hipStreamCaptureModeThreadLocal),
+                          "hipStreamBeginCapture");
+                iteration();
+                hip_check(hipStreamEndCapture(m.stream, &graph), "hipStreamEndCapture");
+                const hipError_t e = hipGraphInstantiate(&m.step_graph, graph, nullptr,
+                                                         nullptr, 0);
+                (void)hipGraphDestroy(graph);
+                hip_check(e, "hipGraphInstantiate");
+            }
+            for (size_t i = 0; i < steps; i++)
+                hip_check(hipGraphLaunch(m.step_graph, m.stream), "hipGraphLaunch");
         }
     }
     hip_check(hipEventRecord(m.decode_end, m.stream), "hipEventRecord");

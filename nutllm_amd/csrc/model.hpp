@@ -59,6 +59,9 @@ struct nut_model {
     // Step workspace.
     nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
     nut::DeviceBuffer xn, attn_part; // fast step kernels
+    // One greedy iteration (classifier, argmax, decode step) captured as a
+    // graph for the generation cache; replayed once per generated token.
+    hipGraphExec_t step_graph = nullptr;
     nut::DeviceBuffer part_val, part_idx, state, tokens, prompt;
     hipStream_t stream = nullptr;
     hipEvent_t decode_begin = nullptr, decode_end = nullptr;

@@ -327,3 +327,22 @@ def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
         ids, _ = dev.generate(prompt, 8)
         ref_ids, _, _ = om.generate(prompt, 8)
         assert ids == ref_ids
+
+
+def test_tinyllama_int4_graph_replays_match_eager(gpu, tinyllama_int4):
+    """A 60-token prompt is past the token kernel's fused attention, so
+    generation replays a captured graph of one greedy iteration per token.
+    Two graph runs, with eager step-kernel work between them, give the ids
+    of the eager path and of the oracle."""
+    model, _, _, dev = tinyllama_int4
+    prompt = gpu.synth_tokens(13, model.config.vocab_size, 60)
+    om = O.oracle_model(model)
+    ref, _, _ = om.generate(prompt, 8)
+    dev.set_path(0)
+    first, _ = dev.generate(prompt, 8)
+    dev.set_path(1)
+    eager, _ = dev.generate(prompt, 8)
+    dev.set_path(0)
+    second, _ = dev.generate(prompt, 8)
+    assert eager == ref
+    assert first == ref and second == ref
