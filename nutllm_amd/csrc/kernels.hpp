@@ -93,12 +93,17 @@ void launch_pick_token(const DecodeShape &s, const float *part_val,
                        const int *part_idx, int parts, StepState *state,
                        int *tokens, hipStream_t stream);
 // Fast step kernels (step.hip): layers whose matrices all use 32-wide
-// blocks along whole rows, head_dim 64 or 128.
+// blocks along whole rows, head_dim 64 or 128, 1, 2, 4 or 8 query heads per
+// KV head. attn_part holds step_attn_part_words(s) words, every byte 0xff
+// before the first step; attn_count holds 2 * heads ints, zero before the
+// first step (the kernels keep both consistent from then on).
 struct StepBuffers {
-    float *hidden, *query, *context, *act, *xn, *attn_part;
+    float *hidden, *query, *context, *act;
+    uint64_t *attn_part;
+    int *attn_count;
 };
 bool step_fast_supported(const DecodeShape &s, const LayerView &w);
-size_t step_attn_part_floats(const DecodeShape &s);
+size_t step_attn_part_words(const DecodeShape &s);
 void launch_layer_fast(const DecodeShape &s, const LayerView &w,
                        const float2 *rope, const int *length, float *k_layer,
                        float *v_layer, const StepBuffers &b,

@@ -95,9 +95,13 @@ void drop_graph(nut_model &m)
 // Workspace of the fast step kernels (allocated before any capture).
 void prepare_fast_steps(nut_model &m)
 {
-    if (m.xn.get() == nullptr) {
-        m.xn.allocate(std::max(m.shape.dim, m.shape.ffn_dim) * sizeof(float));
-        m.attn_part.allocate(step_attn_part_floats(m.shape) * sizeof(float));
+    if (m.attn_count.get() == nullptr) {
+        const size_t part = step_attn_part_words(m.shape) * sizeof(uint64_t);
+        const size_t count = 2 * m.shape.heads * sizeof(int);
+        m.attn_part.allocate(part);
+        m.attn_count.allocate(count);
+        hip_check(hipMemsetAsync(m.attn_part.get(), 0xff, part, m.stream), "hipMemsetAsync");
+        hip_check(hipMemsetAsync(m.attn_count.get(), 0, count, m.stream), "hipMemsetAsync");
     }
 }
 
@@ -113,7 +117,7 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
         prepare_fast_steps(m);
         const StepBuffers b{m.hidden.as<float>(), m.query.as<float>(),
                             m.context.as<float>(), m.act.as<float>(),
-                            m.xn.as<float>(), m.attn_part.as<float>()};
+                            m.attn_part.as<uint64_t>(), m.attn_count.as<int>()};
         for (size_t l = 0; l < m.layers.size(); l++)
             launch_layer_fast(s, m.layers[l].view, m.rope.as<float2>(),
                               kv.device_length.as<int>(),

@@ -58,7 +58,7 @@ struct nut_model {
 
     // Step workspace.
     nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
-    nut::DeviceBuffer xn, attn_part; // fast step kernels
+    nut::DeviceBuffer attn_part, attn_count; // fast step kernels
     // One greedy iteration (classifier, argmax, decode step) captured as a
     // graph for the generation cache; replayed once per generated token.
     hipGraphExec_t step_graph = nullptr;

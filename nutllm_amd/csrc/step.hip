@@ -1,20 +1,25 @@
 // step.hip — fast kernels of one decode step (decode_quantized_token,
 // src/quant_model.cpp:158-206) for layers whose matrices use 32-wide quant
-// blocks along whole rows. Per layer:
-//   norm        xn = rmsnorm(h) * attention_norm          (one workgroup)
-//   qkv         Q/K/V rows of xn, RoPE, K/V into the cache at *length
-//   attn_split  split-K attention: 64-position chunks of one head per
-//               workgroup, partial (max, sum, context) per chunk
-//   attn_merge  per head: merge the chunks into the context vector
-//   wo          h += Wo ctx
-//   norm        xn = rmsnorm(h) * ffn_norm
-//   gate_up     act = silu(Wg xn) * (Wu xn)
-//   down        h += W2 act
-// The matvecs stream rows like the standalone matvec: a wave owns R rows
-// (an even count, so a RoPE pair stays in one wave), each lane issues its
-// 16-byte chunk of every row and its x chunk together, x chunk sums are
-// formed in registers, and the R row sums are reduced with DPP.
+// blocks along whole rows. Five launches per layer:
+//   qkv        xn = rmsnorm(h) * attention_norm folded into the Q/K/V
+//              rows, RoPE, K/V into the cache at *length
+//   attention  one workgroup per (KV head, split of the positions) for all
+//              query heads of the group; online softmax over 32-position
+//              chunks; the last workgroup of a KV head to finish merges
+//              the splits into the context vectors
+//   wo         h += Wo ctx
+//   gate_up    act = silu(Wg xn) * (Wu xn), xn = rmsnorm(h) * ffn_norm
+//   down       h += W2 act
+// The matvecs stream rows: a wave owns R rows (an even count, so a RoPE
+// pair stays in one wave), each lane issues its 16-byte chunk of every row
+// with nontemporal loads, and the R row sums are reduced with DPP. The
+// workgroup stages x (times the norm weights) once in LDS, which keeps the
+// x reads of every wave off the L1; the RMSNorm scalar factors out of the
+// dot: sum_k q_k s (x_k w_k) r = r * sum_k q_k s (x_k w_k) with
+// r = 1 / sqrt(mean(x^2) + 1e-5) (src/ops.cpp:111-134).
 // Every kernel returns at once when the step state says the loop ended.
+#include <algorithm>
+
 #include "kernels.hpp"
 #include "runtime.hpp"
 
@@ -24,8 +29,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kRows = 2;      // rows per wave
-constexpr int kChunk = 64;    // positions per attention split
+constexpr int kAttnChunk = 32;    // positions per attention chunk (8 per wave)
+constexpr int kAttnMaxSplits = 32;
+constexpr int kDppRowRor8 = 0x128; // row_ror:8, lane i <- lane i ^ 8 in a row
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -35,41 +41,99 @@ __device__ __forceinline__ uint4 load_stream(const uint8_t *p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// sum_k q_k x_k s over rows row0 .. row0 + kRows - 1 of m (rows past the end
-// re-read the last row), every lane gets all sums.
-template <int QT>
-__device__ __forceinline__ void rows_dot(const QMat &m, int row0, const float *x,
-                                         float (&out)[kRows])
+// Pointers of rows row0 .. row0 + n - 1 of m (rows past the end re-read the
+// last row) into slots base .. base + n - 1.
+template <int QT, int R>
+__device__ __forceinline__ void row_ptrs(const QMat &m, int row0, int base, int n,
+                                         const uint8_t *(&rp)[R],
+                                         const uint16_t *(&sp)[R])
 {
-    constexpr int CW = QT == 1 ? 32 : 16;
-    constexpr float kBias = QT == 1 ? 8.0f : 128.0f;
-    const int lane = threadIdx.x & (kWave - 1);
     const int row_bytes = QT == 1 ? m.cols / 2 : m.cols;
-    const int chunks = row_bytes / 16;
     const int bpr = m.cols / 32;
-    const uint8_t *rp[kRows];
-    const uint16_t *sp[kRows];
 #pragma unroll
-    for (int r = 0; r < kRows; r++) {
-        const int rr = min(row0 + r, m.rows - 1);
-        rp[r] = m.data + size_t(rr) * row_bytes;
-        sp[r] = m.scales + size_t(rr) * bpr;
-    }
-    float acc[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; r++)
-        acc[r] = 0.0f;
-    for (int c = lane; c < chunks; c += kWave) {
-        const int block = QT == 1 ? c : (c >> 1);
-        uint4 w[kRows];
-        float s[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; r++) {
-            w[r] = load_stream(rp[r] + 16 * c);
-            s[r] = half_bits_to_float(sp[r][block]);
+    for (int r = 0; r < R; r++)
+        if (r >= base && r < base + n) {
+            const int rr = min(row0 + r - base, m.rows - 1);
+            rp[r] = m.data + size_t(rr) * row_bytes;
+            sp[r] = m.scales + size_t(rr) * bpr;
         }
+}
+
+// Weights per 16-byte chunk, and floats per chunk of the staged x (padded
+// by 4 so that the 16-byte reads of 8 consecutive lanes, one chunk apart,
+// fall in distinct LDS banks).
+template <int QT> constexpr int chunk_cw() { return QT == 1 ? 32 : 16; }
+template <int QT> constexpr int chunk_xs() { return chunk_cw<QT>() + 4; }
+
+// LDS bytes of the staged x of a matvec with `cols` columns.
+template <int QT> size_t staged_x_bytes(int cols)
+{
+    return size_t(cols / chunk_cw<QT>()) * chunk_xs<QT>() * sizeof(float);
+}
+
+// out[r] = sum_k q_k s x'_k over row r of R rows (pointers rp / sp, `cols`
+// columns), x'_k = x_k * nw_k when NORM, then times the RMS factor of x;
+// every lane gets all sums. Every wave of the workgroup calls it (`active`
+// false for waves without rows): the workgroup stages x' once into LDS (xs,
+// staged_x_bytes) and reduces sum x^2 in red[kWaves]; each wave issues its
+// first weight chunks before the staging, so they load meanwhile.
+template <int QT, int R, bool NORM>
+__device__ __forceinline__ void rows_matvec(const uint8_t *const (&rp)[R],
+                                            const uint16_t *const (&sp)[R], int cols,
+                                            const float *x, const float *nw, bool active,
+                                            float *xs, float *red, float (&out)[R])
+{
+    constexpr int CW = chunk_cw<QT>(), XS = chunk_xs<QT>();
+    constexpr float kBias = QT == 1 ? 8.0f : 128.0f;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int chunks = cols / CW;
+    uint4 w0[R];
+    float s0[R];
+    const bool first = active && lane < chunks;
+    if (first) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            w0[r] = load_stream(rp[r] + 16 * lane);
+            s0[r] = half_bits_to_float(sp[r][QT == 1 ? lane : lane >> 1]);
+        }
+    }
+    float sq = 0.0f;
+    for (int i = threadIdx.x * 4; i < cols; i += kThreads * 4) {
+        float4 v = *reinterpret_cast<const float4 *>(x + i);
+        if (NORM) {
+            const float4 g = *reinterpret_cast<const float4 *>(nw + i);
+            sq = fmaf(v.x, v.x, sq);
+            sq = fmaf(v.y, v.y, sq);
+            sq = fmaf(v.z, v.z, sq);
+            sq = fmaf(v.w, v.w, sq);
+            v.x *= g.x;
+            v.y *= g.y;
+            v.z *= g.z;
+            v.w *= g.w;
+        }
+        *reinterpret_cast<float4 *>(xs + (i / CW) * XS + i % CW) = v;
+    }
+    if (NORM) {
+        sq = wave_total(sq);
+        if (lane == 0)
+            red[wave] = sq;
+    }
+    __syncthreads();
+    float scale = 1.0f;
+    if (NORM) {
+        float total = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++)
+            total += red[w];
+        scale = 1.0f / sqrtf(total / float(cols) + 1e-5f);
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        acc[r] = 0.0f;
+    auto chunk = [&](int c, const uint4 (&w)[R], const float (&s)[R]) {
         float xc[CW];
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + c * CW);
+        const float4 *x4 = reinterpret_cast<const float4 *>(xs + c * XS);
 #pragma unroll
         for (int q = 0; q < CW / 4; q++) {
             const float4 v = x4[q];
@@ -83,14 +147,27 @@ __device__ __forceinline__ void rows_dot(const QMat &m, int row0, const float *x
         for (int i = 0; i < CW; i++)
             xsum += xc[i];
 #pragma unroll
-        for (int r = 0; r < kRows; r++) {
+        for (int r = 0; r < R; r++) {
             const float d = QT == 1 ? dot_int4_chunk(w[r], xc) : dot_int8_chunk(w[r], xc);
             acc[r] = fmaf(s[r], d - kBias * xsum, acc[r]);
         }
-    }
+    };
+    if (first)
+        chunk(lane, w0, s0);
+    if (active)
+        for (int c = lane + kWave; c < chunks; c += kWave) {
+            uint4 w[R];
+            float s[R];
 #pragma unroll
-    for (int r = 0; r < kRows; r++)
-        out[r] = wave_total(acc[r]);
+            for (int r = 0; r < R; r++) {
+                w[r] = load_stream(rp[r] + 16 * c);
+                s[r] = half_bits_to_float(sp[r][QT == 1 ? c : c >> 1]);
+            }
+            chunk(c, w, s);
+        }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        out[r] = wave_total(acc[r]) * scale;
 }
 
 __device__ __forceinline__ int wave_id()
@@ -98,218 +175,461 @@ __device__ __forceinline__ int wave_id()
     return __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
 }
 
-// xn = h * (1 / sqrt(mean(h^2) + 1e-5)) * w  (src/ops.cpp:111-134)
-__global__ __launch_bounds__(1024) void norm_kernel(const float *h, const float *w,
-                                                    float *xn, int dim,
-                                                    const StepState *state)
-{
-    if (state->done)
-        return;
-    __shared__ float red[1024 / kWave];
-    float sq = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += 1024)
-        sq = fmaf(h[i], h[i], sq);
-    const float total = block_sum(sq, red, 1024 / kWave);
-    const float scale = 1.0f / sqrtf(total / float(dim) + 1e-5f);
-    for (int i = threadIdx.x; i < dim; i += 1024)
-        xn[i] = h[i] * scale * w[i];
-}
-
-// Q/K/V rows (concatenated: query rows, key rows, value rows), RoPE on the
+// Q/K/V rows of rmsnorm(h) * attention_norm (concatenated: query rows, key
+// rows, value rows; R divides dim and kv_heads * head_dim), RoPE on the
 // query and key pairs at position *length (src/quant_model.cpp:26-37), key
 // and value rows into the layer's cache.
-template <int QT>
+template <int QT, int R>
 __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
-    DecodeShape s, const float *xn, QMat wq, QMat wk, QMat wv, const float2 *rope,
-    const int *length, float *k_layer, float *v_layer, float *query,
-    const StepState *state)
+    DecodeShape s, const float *hidden, const float *norm, QMat wq, QMat wk,
+    QMat wv, const float2 *rope, const int *length, float *k_layer,
+    float *v_layer, float *query, const StepState *state)
 {
+    extern __shared__ float xs[];
+    __shared__ float red[kWaves];
     if (state->done)
         return;
     const int kvd = s.kv_heads * s.head_dim;
-    const int row = wave_id() * kRows;
-    if (row >= s.dim + 2 * kvd)
-        return;
+    const int row = wave_id() * R;
+    const bool active = row < s.dim + 2 * kvd;
     const int which = row < s.dim ? 0 : row < s.dim + kvd ? 1 : 2;
     const int local = which == 0 ? row : which == 1 ? row - s.dim : row - s.dim - kvd;
-    float out[kRows];
-    rows_dot<QT>(which == 0 ? wq : which == 1 ? wk : wv, local, xn, out);
+    const uint8_t *rp[R];
+    const uint16_t *sp[R];
+    row_ptrs<QT, R>(which == 0 ? wq : which == 1 ? wk : wv, local, 0, R, rp, sp);
+    float out[R];
+    rows_matvec<QT, R, true>(rp, sp, s.dim, hidden, norm, active, xs, red, out);
+    if (!active)
+        return;
     const int pos = *length;
     const int head = local / s.head_dim, d = local % s.head_dim;
     if (which < 2) {
-        const float2 cs = rope[size_t(pos) * (s.head_dim / 2) + d / 2];
-        const float even = out[0], odd = out[1];
-        out[0] = fmaf(even, cs.x, -(odd * cs.y));
-        out[1] = fmaf(even, cs.y, odd * cs.x);
+#pragma unroll
+        for (int r = 0; r < R; r += 2) {
+            const float2 cs = rope[size_t(pos) * (s.head_dim / 2) + (d + r) / 2];
+            const float even = out[r], odd = out[r + 1];
+            out[r] = fmaf(even, cs.x, -(odd * cs.y));
+            out[r + 1] = fmaf(even, cs.y, odd * cs.x);
+        }
     }
     if ((threadIdx.x & (kWave - 1)) == 0) {
         float *dst = which == 0 ? query + local
                                 : (which == 1 ? k_layer : v_layer) +
                                       (size_t(head) * s.max_seq + pos) * s.head_dim + d;
-        dst[0] = out[0];
-        dst[1] = out[1];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            dst[r] = out[r];
     }
 }
 
 // y[r] += (W x)[r]  (Wo + residual, W2 + residual)
-template <int QT>
+template <int QT, int R>
 __global__ __launch_bounds__(kThreads) void residual_fast_kernel(
     QMat m, const float *x, float *y, const StepState *state)
 {
+    extern __shared__ float xs[];
     if (state->done)
         return;
-    const int row = wave_id() * kRows;
-    if (row >= m.rows)
-        return;
-    float out[kRows];
-    rows_dot<QT>(m, row, x, out);
-    if ((threadIdx.x & (kWave - 1)) == 0)
+    const int row = wave_id() * R;
+    const uint8_t *rp[R];
+    const uint16_t *sp[R];
+    row_ptrs<QT, R>(m, row, 0, R, rp, sp);
+    float out[R];
+    rows_matvec<QT, R, false>(rp, sp, m.cols, x, nullptr, row < m.rows, xs, nullptr, out);
+    if (row < m.rows && (threadIdx.x & (kWave - 1)) == 0)
 #pragma unroll
-        for (int r = 0; r < kRows; r++)
+        for (int r = 0; r < R; r++)
             if (row + r < m.rows)
                 y[row + r] += out[r];
 }
 
-// act[r] = silu((Wg xn)[r]) * (Wu xn)[r]  (src/quant_model.cpp:197-198)
-template <int QT>
+// act[r] = silu((Wg xn)[r]) * (Wu xn)[r], xn = rmsnorm(h) * ffn_norm
+// (src/quant_model.cpp:194-198); R rows of each matrix per wave.
+template <int QT, int R>
 __global__ __launch_bounds__(kThreads) void gate_up_fast_kernel(
-    QMat wg, QMat wu, const float *xn, float *act, const StepState *state)
+    const float *hidden, const float *norm, QMat wg, QMat wu, float *act,
+    const StepState *state)
 {
+    extern __shared__ float xs[];
+    __shared__ float red[kWaves];
     if (state->done)
         return;
-    const int row = wave_id() * kRows;
-    if (row >= wg.rows)
-        return;
-    float g[kRows], u[kRows];
-    rows_dot<QT>(wg, row, xn, g);
-    rows_dot<QT>(wu, row, xn, u);
-    if ((threadIdx.x & (kWave - 1)) == 0)
+    const int row = wave_id() * R;
+    const uint8_t *rp[2 * R];
+    const uint16_t *sp[2 * R];
+    row_ptrs<QT, 2 * R>(wg, row, 0, R, rp, sp);
+    row_ptrs<QT, 2 * R>(wu, row, R, R, rp, sp);
+    float gu[2 * R];
+    rows_matvec<QT, 2 * R, true>(rp, sp, wg.cols, hidden, norm, row < wg.rows, xs, red, gu);
+    if (row < wg.rows && (threadIdx.x & (kWave - 1)) == 0)
 #pragma unroll
-        for (int r = 0; r < kRows; r++)
-            if (row + r < wg.rows)
-                act[row + r] = g[r] / (1.0f + expf(-g[r])) * u[r];
+        for (int r = 0; r < R; r++)
+            if (row + r < wg.rows) {
+                const float g = gu[r], u = gu[R + r];
+                act[row + r] = g / (1.0f + expf(-g)) * u;
+            }
 }
 
-// Split-K attention (src/quant_model.cpp:68-105 for one chunk of
-// positions): workgroup (head, split) covers positions
-// [split * kChunk, min(n, (split + 1) * kChunk)), n = *length + 1, and
-// writes (max, sum of exp, unnormalised context) for its chunk.
-template <int HD>
-__global__ __launch_bounds__(kThreads) void attn_split_kernel(
+// Sums / max over lane bits 0-2 or 3-5, in every lane.
+__device__ __forceinline__ float sum_lanes_0_2(float v)
+{
+    v += dpp<kDppQuadSwap1>(v, 0.0f);
+    v += dpp<kDppQuadSwap2>(v, 0.0f);
+    return v + dpp<kDppRowHalfMirror>(v, 0.0f);
+}
+
+__device__ __forceinline__ float sum_lanes_3_5(float v)
+{
+    v += dpp<kDppRowRor8>(v, 0.0f);
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
+__device__ __forceinline__ float max_lanes_0_2(float v)
+{
+    v = fmaxf(v, dpp<kDppQuadSwap1>(v, -INFINITY));
+    v = fmaxf(v, dpp<kDppQuadSwap2>(v, -INFINITY));
+    return fmaxf(v, dpp<kDppRowHalfMirror>(v, -INFINITY));
+}
+
+// Tagged words of the split results: (tag << 32) | value bits, stored and
+// loaded at agent scope, so every XCD sees them whatever its L2 holds. A
+// word read with the wrong tag is one whose store has not arrived yet.
+constexpr int kMergeSpin = 1 << 20;
+
+__device__ __forceinline__ void publish(uint64_t *p, float v, uint32_t tag)
+{
+    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t take_word(const uint64_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The value of word w at p once it carries tag (bounded re-polling; NaN if
+// it never does, which shows in the context).
+__device__ __forceinline__ float tagged_value(uint64_t w, const uint64_t *p, uint32_t tag)
+{
+    for (int spin = 0; uint32_t(w >> 32) != tag; spin++) {
+        if (spin >= kMergeSpin)
+            return __builtin_nanf("");
+        __builtin_amdgcn_s_sleep(1);
+        w = take_word(p);
+    }
+    return __uint_as_float(uint32_t(w));
+}
+
+// Attention of query heads [G row, G row + G), row = blockIdx.x, over
+// positions [0, n), n = *length + 1 (src/quant_model.cpp:68-105); the G
+// heads share one KV head. The n positions form 32-position chunks, dealt
+// in equal runs to at most gridDim.y splits.
+// Workgroup (row, split) loads up to PF chunks at once and runs an online
+// softmax over each such group: lane (pl = lane % 8, part = lane / 8) of
+// wave w holds position 8 w + pl of every chunk, dims
+// [part * HD / 8, (part + 1) * HD / 8) of its K and V rows, and the running
+// max, sum and context of each head over its positions. One split writes
+// the context directly; otherwise each split publishes (max, sum,
+// unnormalised context) and the workgroup that completes the count of its
+// row merges them:
+//   ctx = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
+// counts[row] counts arrivals over all launches and counts[rows + row] holds
+// its value at the start of this launch (the base): a workgroup whose
+// ticket is base + splits - 1 is the last, and moves the base on. The base
+// also tags this launch's words, so the merge needs no memory fence: it
+// re-reads a word until the word carries the tag.
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) void attention_kernel(
     DecodeShape s, const float *query, const float *k_layer, const float *v_layer,
-    const int *length, float *part, int max_splits, const StepState *state)
+    const int *length, uint64_t *o_part, uint64_t *ml_part, int *counts,
+    float *context, const StepState *state)
 {
     if (state->done)
         return;
-    __shared__ float qs[HD];
-    __shared__ float sc[kChunk];
-    __shared__ float red[kWaves];
-    __shared__ float ctx_part[kThreads / (HD / 4)][HD];
-    const int head = blockIdx.x, split = blockIdx.y;
+    constexpr int S = HD / 8;
+    // chunks in flight: four while q, the context and the K/V rows fit the
+    // register file
+    constexpr int PF = 2 * G * S + 8 * S <= 224 ? 4 : 2;
+    constexpr int OUT = (G * HD + kThreads - 1) / kThreads;
+    const int row = blockIdx.x, split = blockIdx.y;
+    const int kvh = row * G / (s.heads / s.kv_heads);
     const int n = *length + 1;
-    const int p0 = split * kChunk;
-    if (p0 >= n)
+    const int chunks = (n + kAttnChunk - 1) / kAttnChunk;
+    const int want = min(int(gridDim.y), chunks);
+    const int per = (chunks + want - 1) / want;
+    const int splits = (chunks + per - 1) / per;
+    if (split >= splits)
         return; // workgroup-uniform
-    const int count = min(kChunk, n - p0);
-    const int kvh = head / (s.heads / s.kv_heads);
-    const float *kg = k_layer + (size_t(kvh) * s.max_seq + p0) * HD;
-    const float *vg = v_layer + (size_t(kvh) * s.max_seq + p0) * HD;
-    for (int i = threadIdx.x; i < HD; i += kThreads)
-        qs[i] = query[head * HD + i];
-    __syncthreads();
-    // scores: thread (p = tid / 4, quarter = tid % 4) dots a quarter row
-    {
-        const int p = threadIdx.x >> 2, quarter = threadIdx.x & 3;
-        constexpr int Q4 = HD / 16; // float4 per quarter row
-        float dot = 0.0f;
-        if (p < count) {
-            const float4 *kr = reinterpret_cast<const float4 *>(kg + size_t(p) * HD) +
-                               quarter * Q4;
-            const float4 *q4 = reinterpret_cast<const float4 *>(qs) + quarter * Q4;
+    const int c_begin = split * per, c_end = min(chunks, c_begin + per);
+    const int base = splits > 1 ? __hip_atomic_load(counts + gridDim.x + row, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                                : 0;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int pl = lane & 7, part = lane >> 3, prow = wave * 8 + pl;
+
+    __shared__ float wmax[2][kWaves][G];
+    __shared__ float red[kWaves][G][HD];
+    __shared__ float lred[kWaves][G];
+    __shared__ float mls[kAttnMaxSplits][G][2];
+    __shared__ float fw[kAttnMaxSplits][G];
+    __shared__ int last;
+
+    float q[G][S];
 #pragma unroll
-            for (int j = 0; j < Q4; j++) {
-                const float4 k = kr[j], q = q4[j];
-                dot = fmaf(q.x, k.x, dot);
-                dot = fmaf(q.y, k.y, dot);
-                dot = fmaf(q.z, k.z, dot);
-                dot = fmaf(q.w, k.w, dot);
+    for (int g = 0; g < G; g++) {
+        const float4 *src = reinterpret_cast<const float4 *>(
+            query + size_t(row * G + g) * HD + part * S);
+#pragma unroll
+        for (int j = 0; j < S / 4; j++) {
+            const float4 v = src[j];
+            q[g][4 * j] = v.x;
+            q[g][4 * j + 1] = v.y;
+            q[g][4 * j + 2] = v.z;
+            q[g][4 * j + 3] = v.w;
+        }
+    }
+    const float *kbase = k_layer + size_t(kvh) * s.max_seq * HD + part * S;
+    const float *vbase = v_layer + size_t(kvh) * s.max_seq * HD + part * S;
+    float m[G], l[G], acc[G][S];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < S; i++)
+            acc[g][i] = 0.0f;
+    }
+    for (int c0 = c_begin, group = 0; c0 < c_end; c0 += PF, group++) {
+        float kb[PF][S], vb[PF][S];
+        bool valid[PF];
+#pragma unroll
+        for (int j = 0; j < PF; j++) {
+            const int p = (c0 + j) * kAttnChunk + prow;
+            valid[j] = c0 + j < c_end && p < n;
+            if (valid[j]) {
+                const float4 *k4 = reinterpret_cast<const float4 *>(kbase + size_t(p) * HD);
+                const float4 *v4 = reinterpret_cast<const float4 *>(vbase + size_t(p) * HD);
+#pragma unroll
+                for (int i = 0; i < S / 4; i++) {
+                    const float4 a = k4[i], b = v4[i];
+                    kb[j][4 * i] = a.x, kb[j][4 * i + 1] = a.y;
+                    kb[j][4 * i + 2] = a.z, kb[j][4 * i + 3] = a.w;
+                    vb[j][4 * i] = b.x, vb[j][4 * i + 1] = b.y;
+                    vb[j][4 * i + 2] = b.z, vb[j][4 * i + 3] = b.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < S; i++)
+                    kb[j][i] = vb[j][i] = 0.0f;
             }
         }
-        dot += dpp<kDppQuadSwap1>(dot, 0.0f);
-        dot += dpp<kDppQuadSwap2>(dot, 0.0f);
-        if (quarter == 0 && p < kChunk)
-            sc[p] = p < count ? dot * s.attn_scale : -INFINITY;
-    }
-    __syncthreads();
-    float m = -INFINITY;
-    if (threadIdx.x < kWave) {
-        m = wave_maximum(threadIdx.x < kChunk ? sc[threadIdx.x] : -INFINITY);
-        const float e = threadIdx.x < count ? expf(sc[threadIdx.x] - m) : 0.0f;
-        sc[threadIdx.x] = e;
-        const float l = wave_total(e);
-        if (threadIdx.x == 0) {
-            red[0] = m;
-            red[1] = l;
+        // scores of the group's positions, and their max per head
+        float sc[PF][G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float gm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < PF; j++) {
+                sc[j][g] = -INFINITY;
+                if (c0 + j < c_end) { // workgroup-uniform
+                    float d = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < S; i++)
+                        d = fmaf(q[g][i], kb[j][i], d);
+                    d = sum_lanes_3_5(d);
+                    sc[j][g] = valid[j] ? d * s.attn_scale : -INFINITY;
+                }
+                gm = fmaxf(gm, sc[j][g]);
+            }
+            gm = max_lanes_0_2(gm);
+            if (lane == 0)
+                wmax[group & 1][wave][g] = gm;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float cm = wmax[group & 1][0][g];
+#pragma unroll
+            for (int w = 1; w < kWaves; w++)
+                cm = fmaxf(cm, wmax[group & 1][w][g]);
+            const float mn = fmaxf(m[g], cm);
+            const float alpha = expf(m[g] - mn);
+            m[g] = mn;
+            l[g] *= alpha;
+#pragma unroll
+            for (int i = 0; i < S; i++)
+                acc[g][i] *= alpha;
+#pragma unroll
+            for (int j = 0; j < PF; j++)
+                if (c0 + j < c_end) { // workgroup-uniform
+                    const float e = valid[j] ? expf(sc[j][g] - mn) : 0.0f;
+                    l[g] += e;
+#pragma unroll
+                    for (int i = 0; i < S; i++)
+                        acc[g][i] = fmaf(e, vb[j][i], acc[g][i]);
+                }
         }
     }
+    // sum the lanes' positions: within the wave, then over the waves
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int i = 0; i < S; i++)
+            acc[g][i] = sum_lanes_0_2(acc[g][i]);
+        l[g] = sum_lanes_0_2(l[g]);
+        if (pl == 0) {
+#pragma unroll
+            for (int i = 0; i < S; i++)
+                red[wave][g][part * S + i] = acc[g][i];
+        }
+        if (lane == 0)
+            lred[wave][g] = l[g];
+    }
     __syncthreads();
-    // context: thread (group = tid / (HD / 4), quad = tid % (HD / 4))
-    // accumulates positions group, group + groups, ...
-    constexpr int QUADS = HD / 4, GROUPS = kThreads / QUADS;
-    const int quad = threadIdx.x % QUADS, group = threadIdx.x / QUADS;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int p = group; p < count; p += GROUPS) {
-        const float w = sc[p];
-        const float4 v = reinterpret_cast<const float4 *>(vg + size_t(p) * HD)[quad];
-        acc.x = fmaf(w, v.x, acc.x);
-        acc.y = fmaf(w, v.y, acc.y);
-        acc.z = fmaf(w, v.z, acc.z);
-        acc.w = fmaf(w, v.w, acc.w);
-    }
-    *reinterpret_cast<float4 *>(&ctx_part[group][4 * quad]) = acc;
-    __syncthreads();
-    float *out = part + (size_t(head) * max_splits + split) * (HD + 2);
-    for (int d = threadIdx.x; d < HD; d += kThreads) {
-        float sum = 0.0f;
-        for (int g = 0; g < GROUPS; g++)
-            sum += ctx_part[g][d];
-        out[2 + d] = sum;
-    }
-    if (threadIdx.x == 0) {
-        out[0] = red[0];
-        out[1] = red[1];
-    }
-}
-
-// context[head] = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s
-template <int HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(const float *part,
-                                                        const int *length,
-                                                        float *context,
-                                                        int max_splits,
-                                                        const StepState *state)
-{
-    if (state->done)
+    if (splits == 1) {
+        for (int t = threadIdx.x; t < G * HD; t += kThreads) {
+            const int g = t / HD, d = t % HD;
+            float o = 0.0f, lt = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                o += red[w][g][d];
+                lt += lred[w][g];
+            }
+            context[size_t(row * G) * HD + t] = o / lt;
+        }
         return;
-    const int head = blockIdx.x;
-    const int splits = (*length + 1 + kChunk - 1) / kChunk;
-    const float *p = part + size_t(head) * max_splits * (HD + 2);
-    float mx = -INFINITY;
-    for (int s = 0; s < splits; s++)
-        mx = fmaxf(mx, p[s * (HD + 2)]);
-    float l = 0.0f, o = 0.0f;
-    for (int s = 0; s < splits; s++) {
-        const float f = expf(p[s * (HD + 2)] - mx);
-        l = fmaf(p[s * (HD + 2) + 1], f, l);
-        o = fmaf(p[s * (HD + 2) + 2 + threadIdx.x], f, o);
     }
-    context[head * HD + threadIdx.x] = o / l;
+    const uint32_t tag = uint32_t(base);
+    const size_t slot = size_t(row) * gridDim.y + split;
+    for (int t = threadIdx.x; t < G * HD; t += kThreads) {
+        const int g = t / HD, d = t % HD;
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++)
+            o += red[w][g][d];
+        publish(o_part + slot * G * HD + t, o, tag);
+    }
+    if (threadIdx.x < G) {
+        float lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++)
+            lt += lred[w][threadIdx.x];
+        // every lane tracked every group max, so m[g] is the split's max
+        float mg = m[0];
+#pragma unroll
+        for (int g = 1; g < G; g++)
+            if (int(threadIdx.x) == g)
+                mg = m[g];
+        publish(ml_part + (slot * G + threadIdx.x) * 2, mg, tag);
+        publish(ml_part + (slot * G + threadIdx.x) * 2 + 1, lt, tag);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int ticket = __hip_atomic_fetch_add(counts + row, 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        last = ticket - base == splits - 1;
+        if (ticket - base == splits - 1)
+            __hip_atomic_store(counts + gridDim.x + row, base + splits, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last)
+        return;
+    // merge: every word is requested at once; the weights
+    // exp(m_s - M) / L of every (split, head) go through LDS meanwhile
+    const uint64_t *ml = ml_part + size_t(row) * gridDim.y * G * 2;
+    const uint64_t *op = o_part + size_t(row) * gridDim.y * G * HD;
+    uint64_t a[OUT][kAttnMaxSplits];
+#pragma unroll
+    for (int u = 0; u < OUT; u++) {
+        const int t = threadIdx.x + u * kThreads;
+#pragma unroll
+        for (int j = 0; j < kAttnMaxSplits; j++)
+            a[u][j] = t < G * HD && j < splits ? take_word(op + size_t(j) * G * HD + t) : 0;
+    }
+    if (threadIdx.x < splits * G) {
+        const int sp = threadIdx.x / G, g = threadIdx.x % G;
+        const uint64_t *p = ml + threadIdx.x * 2;
+        const uint64_t w0 = take_word(p), w1 = take_word(p + 1);
+        mls[sp][g][0] = tagged_value(w0, p, tag);
+        mls[sp][g][1] = tagged_value(w1, p + 1, tag);
+    }
+    __syncthreads();
+    if (threadIdx.x < kAttnMaxSplits * G) {
+        const int sp = threadIdx.x / G, g = threadIdx.x % G;
+        float weight = 0.0f;
+        if (sp < splits) {
+            float mx = -INFINITY;
+            for (int j = 0; j < splits; j++)
+                mx = fmaxf(mx, mls[j][g][0]);
+            float total = 0.0f;
+            for (int j = 0; j < splits; j++)
+                total = fmaf(mls[j][g][1], expf(mls[j][g][0] - mx), total);
+            weight = expf(mls[sp][g][0] - mx) / total;
+        }
+        fw[sp][g] = weight;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < OUT; u++) {
+        const int t = threadIdx.x + u * kThreads;
+        if (t < G * HD) {
+            const int g = t / HD;
+            float o = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kAttnMaxSplits; j++)
+                if (j < splits)
+                    o = fmaf(tagged_value(a[u][j], op + size_t(j) * G * HD + t, tag), fw[j][g], o);
+            context[size_t(row * G) * HD + t] = o;
+        }
+    }
 }
 
-int blocks_for_rows(int rows)
+int blocks_for_rows(int rows, int per_wave)
 {
-    const int waves = (rows + kRows - 1) / kRows;
+    const int waves = (rows + per_wave - 1) / per_wave;
     return (waves + kWaves - 1) / kWaves;
+}
+
+// Query heads per attention workgroup: two of head_dim 64, one of 128.
+int attention_group(const DecodeShape &s)
+{
+    return s.head_dim == 64 && (s.heads / s.kv_heads) % 2 == 0 ? 2 : 1;
+}
+
+// Splits of the attention grid: enough workgroups for the chip's 256 CUs,
+// at most kAttnMaxSplits, at most one per chunk of max_seq.
+int attention_splits(const DecodeShape &s)
+{
+    const int rows = s.heads / attention_group(s);
+    const int chunks = (s.max_seq + kAttnChunk - 1) / kAttnChunk;
+    const int want = (256 + rows - 1) / rows;
+    return std::max(1, std::min({want, kAttnMaxSplits, chunks}));
+}
+
+template <int HD, int G>
+void launch_attention(const DecodeShape &s, const float *k_layer, const float *v_layer,
+                      const int *length, const StepBuffers &b, const StepState *state,
+                      hipStream_t stream)
+{
+    const int splits = attention_splits(s);
+    uint64_t *o_part = b.attn_part;
+    uint64_t *ml_part = b.attn_part + size_t(s.heads) * splits * HD;
+    hipLaunchKernelGGL((attention_kernel<HD, G>), dim3(s.heads / G, splits),
+                       dim3(kThreads), 0, stream, s, b.query, k_layer, v_layer, length,
+                       o_part, ml_part, b.attn_count, b.context, state);
+}
+
+template <int HD>
+void launch_attention_g(const DecodeShape &s, const float *k_layer, const float *v_layer,
+                        const int *length, const StepBuffers &b, const StepState *state,
+                        hipStream_t stream)
+{
+    if (attention_group(s) == 2)
+        launch_attention<HD, 2>(s, k_layer, v_layer, length, b, state, stream);
+    else
+        launch_attention<HD, 1>(s, k_layer, v_layer, length, b, state, stream);
 }
 
 template <int QT, int HD>
@@ -319,26 +639,32 @@ void launch_layer_fast_t(const DecodeShape &s, const LayerView &w,
                          const StepState *state, hipStream_t stream)
 {
     const int kvd = s.kv_heads * s.head_dim;
-    const int max_splits = (s.max_seq + kChunk - 1) / kChunk;
-    hipLaunchKernelGGL(norm_kernel, dim3(1), dim3(1024), 0, stream, b.hidden,
-                       w.attention_norm, b.xn, s.dim, state);
-    hipLaunchKernelGGL((qkv_fast_kernel<QT>), dim3(blocks_for_rows(s.dim + 2 * kvd)),
-                       dim3(kThreads), 0, stream, s, b.xn, w.query, w.key, w.value,
-                       rope, length, k_layer, v_layer, b.query, state);
-    hipLaunchKernelGGL((attn_split_kernel<HD>), dim3(s.heads, max_splits),
-                       dim3(kThreads), 0, stream, s, b.query, k_layer, v_layer,
-                       length, b.attn_part, max_splits, state);
-    hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(s.heads), dim3(HD), 0, stream,
-                       b.attn_part, length, b.context, max_splits, state);
-    hipLaunchKernelGGL((residual_fast_kernel<QT>), dim3(blocks_for_rows(s.dim)),
-                       dim3(kThreads), 0, stream, w.output, b.context, b.hidden,
-                       state);
-    hipLaunchKernelGGL(norm_kernel, dim3(1), dim3(1024), 0, stream, b.hidden,
-                       w.ffn_norm, b.xn, s.dim, state);
-    hipLaunchKernelGGL((gate_up_fast_kernel<QT>), dim3(blocks_for_rows(s.ffn_dim)),
-                       dim3(kThreads), 0, stream, w.gate, w.up, b.xn, b.act, state);
-    hipLaunchKernelGGL((residual_fast_kernel<QT>), dim3(blocks_for_rows(s.dim)),
-                       dim3(kThreads), 0, stream, w.down, b.act, b.hidden, state);
+    const size_t x_dim = staged_x_bytes<QT>(s.dim), x_ffn = staged_x_bytes<QT>(s.ffn_dim);
+    // four rows per wave where that still gives every CU a workgroup
+    const int qkv_rows = s.dim + 2 * kvd;
+    if (qkv_rows >= 8192 && s.dim % 4 == 0 && kvd % 4 == 0)
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 4>), dim3(blocks_for_rows(qkv_rows, 4)),
+                           dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
+                           w.query, w.key, w.value, rope, length, k_layer, v_layer,
+                           b.query, state);
+    else
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 2>), dim3(blocks_for_rows(qkv_rows, 2)),
+                           dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
+                           w.query, w.key, w.value, rope, length, k_layer, v_layer,
+                           b.query, state);
+    launch_attention_g<HD>(s, k_layer, v_layer, length, b, state, stream);
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2)),
+                       dim3(kThreads), x_dim, stream, w.output, b.context, b.hidden, state);
+    if (s.ffn_dim >= 8192)
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4>), dim3(blocks_for_rows(s.ffn_dim, 4)),
+                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate,
+                           w.up, b.act, state);
+    else
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.ffn_dim, 2)),
+                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate,
+                           w.up, b.act, state);
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2)),
+                       dim3(kThreads), x_ffn, stream, w.down, b.act, b.hidden, state);
     check_launch("decode step");
 }
 
@@ -351,14 +677,19 @@ bool step_fast_supported(const DecodeShape &s, const LayerView &w)
     for (const QMat *m : mats)
         if (!fast_layout(*m) || m->type != w.query.type)
             return false;
-    return (s.head_dim == 64 || s.head_dim == 128) && s.dim <= 16384 &&
-           (s.dim + 2 * s.kv_heads * s.head_dim) % kRows == 0;
+    const int group = s.kv_heads > 0 ? s.heads / s.kv_heads : 0;
+    // the staged x of every matvec fits a workgroup's 64 KB of LDS
+    const int cols = std::max(s.dim, s.ffn_dim);
+    const size_t staged = w.query.type == 1 ? staged_x_bytes<1>(cols) : staged_x_bytes<0>(cols);
+    return (s.head_dim == 64 || s.head_dim == 128) && staged <= 65536 &&
+           s.heads == group * s.kv_heads &&
+           (group == 1 || group == 2 || group == 4 || group == 8) &&
+           s.dim % 2 == 0 && (s.kv_heads * s.head_dim) % 2 == 0;
 }
 
-size_t step_attn_part_floats(const DecodeShape &s)
+size_t step_attn_part_words(const DecodeShape &s)
 {
-    const size_t splits = (size_t(s.max_seq) + kChunk - 1) / kChunk;
-    return size_t(s.heads) * splits * (size_t(s.head_dim) + 2);
+    return size_t(s.heads) * attention_splits(s) * (size_t(s.head_dim) + 2);
 }
 
 void launch_layer_fast(const DecodeShape &s, const LayerView &w,

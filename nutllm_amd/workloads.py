@@ -41,6 +41,14 @@ SHAPES = {
     "llama7b": dict(layers=32, heads=32, dim=4096, head_dim=128,
                     ffn_dim=11008, vocab_size=32000, max_seq=640,
                     eos_token=1, kv_heads=32),
+    # small shapes for the step-kernel parity tests: head_dim 128 with one
+    # query head per KV head, head_dim 64 with four and with two
+    "step_mha128": dict(layers=2, heads=2, dim=256, head_dim=128, ffn_dim=512,
+                        vocab_size=512, max_seq=1200, eos_token=1, kv_heads=2),
+    "step_gqa4": dict(layers=2, heads=8, dim=512, head_dim=64, ffn_dim=768,
+                      vocab_size=512, max_seq=1200, eos_token=1, kv_heads=2),
+    "step_gqa2": dict(layers=2, heads=4, dim=256, head_dim=64, ffn_dim=512,
+                      vocab_size=512, max_seq=1200, eos_token=1, kv_heads=2),
 }
 
 # The named runs: shape, quant type, weight seed, prompt seed, prompt

@@ -346,3 +346,61 @@ def test_tinyllama_int4_graph_replays_match_eager(gpu, tinyllama_int4):
     second, _ = dev.generate(prompt, 8)
     assert eager == ref
     assert first == ref and second == ref
+
+
+STEP_SHAPES = [("step_mha128", 1), ("step_gqa4", 0), ("step_gqa2", 1)]
+
+
+@pytest.mark.parametrize("shape,qtype", STEP_SHAPES,
+                         ids=["mha128-int4", "gqa4-int8", "gqa2-int4"])
+def test_step_kernels_long_context(gpu, shape, qtype):
+    """Step kernels against the oracle at a 1100-token context: RMSNorm
+    folded into the Q/K/V and gate/up matvecs (non-unit norm weights), and
+    attention split over 35 chunks of 32 positions whose splits are merged
+    by the last workgroup of each KV head. Hidden state after the per-token
+    prefill, K/V rows and each decode step of the greedy continuation
+    (rel-L2 1e-5); 8 greedy ids identical."""
+    O.orc().orc_set_threads(16)
+    model = W.build(shape, qtype, 5)
+    c = model.config
+    rng = np.random.default_rng(7)
+    norms = [tuple((1.0 + 0.25 * rng.standard_normal(c.dim)).astype(np.float32)
+                   for _ in range(2)) for _ in range(c.layers)]
+    dev = gpu.DeviceModel(c, qtype)
+    dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
+    for i, mats in enumerate(model.layers):
+        dev.set_layer(i, mats, norms[i][0], norms[i][1])
+    cfg = {n: getattr(c, n) for n, _ in O.OrcConfig._fields_}
+    om = O.OracleModel(cfg, qtype, model.embeddings, model.final_norm,
+                       model.lm_head, model.layers, norms)
+    prompt = gpu.synth_tokens(21, c.vocab_size, 1100)
+    dev.set_path(1)
+    try:
+        cache = gpu.KVCache(c)
+        h = dev.prefill(cache, prompt)
+        om.reset()
+        om_h = om.prefill(prompt)
+        err = rel_l2(h, om_h)
+        print(f"{shape}: prefill hidden rel-L2 {err:.2e}", flush=True)
+        assert err <= TOL
+        for layer in range(c.layers):
+            for kvh in range(c.kv_heads):
+                for p in (0, 550, 1099):
+                    k, v = cache.key_value(layer, kvh, p)
+                    rk, rv = om.kv_row(layer, kvh, p)
+                    assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+        # greedy continuation on both caches (src/generate.cpp:194-207):
+        # every decode step's hidden state, then the device's own loop
+        ref, ho, hd = [], om_h, h
+        for _ in range(8):
+            token = int(np.argmax(om.logits(ho)))
+            if token == c.eos_token:
+                break
+            ref.append(token)
+            ho, hd = om.decode(token), dev.decode(cache, token)
+            assert rel_l2(hd, ho) <= TOL
+        ids, _ = dev.generate(prompt, 8)
+        assert ids == ref
+    finally:
+        dev.set_path(0)
+        dev.close()
