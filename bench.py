@@ -33,9 +33,9 @@ HBM_PEAK_GBS = 8000.0
 PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 
 # HBM bytes one generate launch (16 iterations) moves, from rocprofv3
-# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (scales from a 1 GiB device copy);
-# profiles/token_kernel_tinyllama_int4_decode.md holds the runs.
-MEASURED_TRAFFIC_BYTES = 13_523_878_912
+# counter runs of this bench: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB (the
+# scales read off a 1 GiB device-to-device copy in the same runs).
+MEASURED_TRAFFIC_BYTES = 13_521_548_490
 CPU_SAMPLE_SECONDS = 10.0
 
 
