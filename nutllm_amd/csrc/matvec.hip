@@ -2,30 +2,25 @@
 //
 // Bandwidth-bound, no MFMA. Fast layout (block 32, cols % 32 == 0): a wave
 // owns R consecutive rows; lane l handles 16-byte chunks l, l + 64, ... of
-// each row (one INT4 block or half an INT8 block per chunk). Every lane
-// issues its R row chunks (non-temporal: streamed once) and its x chunk
-// together, sums the x chunk in registers for the offset-binary bias, and
-// the R row sums are reduced with DPP at the end. No LDS, no barrier: the
-// whole matrix is in flight after one round of issue.
+// each row (one INT4 block or half an INT8 block per chunk) and the R row
+// sums are reduced with DPP at the end. Two variants:
+//   staged  the workgroup stages x once in LDS (rows.hpp) and each lane
+//           reads its x chunk from there; the first weight chunk of every
+//           row is requested before the staging, so it loads meanwhile;
+//   direct  each lane reads its x chunk from global memory (through L1);
+//           used when x does not fit 64 KB of LDS.
 // Other layouts (blocks straddling rows, other block sizes) run one row
 // per wave from an LDS copy of x.
 #include "kernels.hpp"
+#include "rows.hpp"
 #include "runtime.hpp"
 
 namespace nut {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / kWave;
-
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint4 load_stream(const uint8_t *p)
-{
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
+constexpr int kThreads = kRowThreads;
+constexpr int kWaves = kRowWaves;
 
 template <int QT, int R>
 __global__ __launch_bounds__(kThreads) void matvec_q_fast(QMat m,
@@ -88,6 +83,24 @@ __global__ __launch_bounds__(kThreads) void matvec_q_fast(QMat m,
         if (lane == 0 && row0 + r < m.rows)
             y[row0 + r] = v;
     }
+}
+
+template <int QT, int R>
+__global__ __launch_bounds__(kThreads) void matvec_q_staged(QMat m, const float *x,
+                                                            float *y)
+{
+    extern __shared__ float xs[];
+    const int row0 = (blockIdx.x * kWaves + threadIdx.x / kWave) * R;
+    const uint8_t *rp[R];
+    const uint16_t *sp[R];
+    row_ptrs<QT, R>(m, row0, 0, R, rp, sp);
+    float out[R];
+    rows_matvec<QT, R, false>(rp, sp, m.cols, x, nullptr, row0 < m.rows, xs, nullptr, out);
+    if (row0 < m.rows && (threadIdx.x & (kWave - 1)) == 0)
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (row0 + r < m.rows)
+                y[row0 + r] = out[r];
 }
 
 __global__ __launch_bounds__(kThreads) void matvec_q_generic(QMat m,
@@ -165,10 +178,33 @@ void launch_fast(const QMat &m, const float *x, float *y, hipStream_t stream)
                        stream, m, x, y);
 }
 
+template <int QT, int R>
+void launch_staged(const QMat &m, const float *x, float *y, hipStream_t stream)
+{
+    const int waves = (m.rows + R - 1) / R;
+    const int blocks = (waves + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL((matvec_q_staged<QT, R>), dim3(blocks), dim3(kThreads),
+                       staged_x_bytes<QT>(m.cols), stream, m, x, y);
+}
+
 void launch_matvec_q(const QMat &m, const float *x, float *y,
                      hipStream_t stream)
 {
-    if (fast_layout(m)) {
+    // INT4 chunks need 32 floats of x per 16 bytes of weights, which keeps
+    // L1 busier than HBM unless x comes from LDS; INT8 chunks need 16, and
+    // below 4096 rows the staging latency costs more than it saves
+    // (measured per shape with rocprofv3)
+    const bool staged = m.type == 1 ? staged_x_bytes<1>(m.cols) <= 65536
+                                    : m.rows >= 4096 && staged_x_bytes<0>(m.cols) <= 65536;
+    if (fast_layout(m) && staged) {
+        // two rows per wave, one where that leaves fewer than 256 workgroups
+        if (m.rows >= 2048)
+            m.type == 1 ? launch_staged<1, 2>(m, x, y, stream)
+                        : launch_staged<0, 2>(m, x, y, stream);
+        else
+            m.type == 1 ? launch_staged<1, 1>(m, x, y, stream)
+                        : launch_staged<0, 1>(m, x, y, stream);
+    } else if (fast_layout(m)) {
         // rows per wave: enough waves to fill 256 CUs, as many rows in
         // flight per wave as that allows
         const int r = m.rows >= 4096 ? 4 : m.rows >= 1024 ? 2 : 1;
