@@ -94,9 +94,13 @@ void launch_pick_token(const DecodeShape &s, const float *part_val,
                        int *tokens, hipStream_t stream);
 // Fast step kernels (step.hip): layers whose matrices all use 32-wide
 // blocks along whole rows, head_dim 64 or 128, 1, 2, 4 or 8 query heads per
-// KV head. attn_part holds step_attn_part_words(s) words, every byte 0xff
-// before the first step; attn_count holds 2 * heads ints, zero before the
-// first step (the kernels keep both consistent from then on).
+// KV head. One launch runs 1 .. kStepTokensMax consecutive tokens at
+// positions *length, *length + 1, ...: hidden, query and context hold a
+// [tokens][dim] row per token, act a [tokens][ffn] row. attn_part holds
+// step_attn_part_words(s) words, every byte 0xff before the first step;
+// attn_count holds 2 * heads * kStepTokensMax ints, zero before the first
+// step (the kernels keep both consistent from then on).
+constexpr int kStepTokensMax = 15;
 struct StepBuffers {
     float *hidden, *query, *context, *act;
     uint64_t *attn_part;
@@ -106,7 +110,7 @@ bool step_fast_supported(const DecodeShape &s, const LayerView &w);
 size_t step_attn_part_words(const DecodeShape &s);
 void launch_layer_fast(const DecodeShape &s, const LayerView &w,
                        const float2 *rope, const int *length, float *k_layer,
-                       float *v_layer, const StepBuffers &b,
+                       float *v_layer, const StepBuffers &b, int tokens,
                        const StepState *state, hipStream_t stream);
 
 // Tiny state writers, enqueued on the stream (graph-safe, no memset).

@@ -97,7 +97,7 @@ void prepare_fast_steps(nut_model &m)
 {
     if (m.attn_count.get() == nullptr) {
         const size_t part = step_attn_part_words(m.shape) * sizeof(uint64_t);
-        const size_t count = 2 * m.shape.heads * sizeof(int);
+        const size_t count = 2 * size_t(m.shape.heads) * kStepTokensMax * sizeof(int);
         m.attn_part.allocate(part);
         m.attn_count.allocate(count);
         hip_check(hipMemsetAsync(m.attn_part.get(), 0xff, part, m.stream), "hipMemsetAsync");
@@ -122,7 +122,7 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
             launch_layer_fast(s, m.layers[l].view, m.rope.as<float2>(),
                               kv.device_length.as<int>(),
                               kv.keys.as<float>() + l * layer_elems,
-                              kv.values.as<float>() + l * layer_elems, b, state,
+                              kv.values.as<float>() + l * layer_elems, b, 1, state,
                               m.stream);
         launch_finish_step(state, kv.device_length.as<int>(), m.stream);
         return;
@@ -139,6 +139,45 @@ void enqueue_step(nut_model &m, nut_kvcache &kv, const int *token_ptr)
 }
 
 void sync(nut_model &m) { hip_check(hipStreamSynchronize(m.stream), "hipStreamSynchronize"); }
+
+// Tokens [0, count) (device ids in m.prompt) through the step kernels in
+// chunks of up to kStepTokensMax consecutive tokens per launch: every
+// weight row is streamed once per chunk instead of once per token, and the
+// arithmetic of each token is the decode step's. The last token's hidden
+// state lands in m.hidden; kv.device_length ends at count.
+void prefill_steps(nut_model &m, nut_kvcache &kv, size_t count)
+{
+    const DecodeShape &s = m.shape;
+    prepare_fast_steps(m);
+    if (m.mt_hidden.get() == nullptr) {
+        m.mt_hidden.allocate(size_t(kStepTokensMax) * s.dim * sizeof(float));
+        m.mt_query.allocate(size_t(kStepTokensMax) * s.dim * sizeof(float));
+        m.mt_context.allocate(size_t(kStepTokensMax) * s.dim * sizeof(float));
+        m.mt_act.allocate(size_t(kStepTokensMax) * s.ffn_dim * sizeof(float));
+    }
+    StepState *state = m.state.as<StepState>();
+    launch_reset_state(state, 0, m.stream);
+    const StepBuffers b{m.mt_hidden.as<float>(), m.mt_query.as<float>(),
+                        m.mt_context.as<float>(), m.mt_act.as<float>(),
+                        m.attn_part.as<uint64_t>(), m.attn_count.as<int>()};
+    const size_t layer_elems = kv.layer_elements();
+    size_t t = 0;
+    for (size_t start = 0; start < count; start += t) {
+        t = std::min<size_t>(kStepTokensMax, count - start);
+        launch_set_int(kv.device_length.as<int>(), int(start), m.stream);
+        launch_embed_rows(m.embeddings.as<float>(), m.prompt.as<int>() + start,
+                          m.mt_hidden.as<float>(), int(t), s.dim, m.stream);
+        for (size_t l = 0; l < m.layers.size(); l++)
+            launch_layer_fast(s, m.layers[l].view, m.rope.as<float2>(),
+                              kv.device_length.as<int>(),
+                              kv.keys.as<float>() + l * layer_elems,
+                              kv.values.as<float>() + l * layer_elems, b, int(t), state,
+                              m.stream);
+    }
+    hip_check(hipMemcpyAsync(m.hidden.get(), m.mt_hidden.as<float>() + (t - 1) * s.dim,
+                             s.dim * sizeof(float), hipMemcpyDeviceToDevice, m.stream),
+              "hipMemcpyAsync");
+}
 
 // Prompts of at least this many tokens run as a batch (GEMM prefill).
 constexpr size_t kPrefillGemmMin = 16;
@@ -545,6 +584,8 @@ void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
                   "hipMemcpyAsync");
         if (use_prefill_gemm(m, valid)) {
             prefill_batch(m, kv, valid);
+        } else if (m.path != 2 && valid > 1 && fast_steps(m)) {
+            prefill_steps(m, kv, valid);
         } else if (use_token_kernel(m, valid)) {
             run_token_kernel(m, kv, 0, valid, false, m.prompt.as<int>(), nullptr,
                              m.hidden.as<float>());

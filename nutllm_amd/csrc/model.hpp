@@ -59,6 +59,8 @@ struct nut_model {
     // Step workspace.
     nut::DeviceBuffer hidden, query, context, act, logits, scratch_hidden;
     nut::DeviceBuffer attn_part, attn_count; // fast step kernels
+    // Prompt chunks on the step kernels: kStepTokensMax rows each.
+    nut::DeviceBuffer mt_hidden, mt_query, mt_context, mt_act;
     // One greedy iteration (classifier, argmax, decode step) captured as a
     // graph for the generation cache; replayed once per generated token.
     hipGraphExec_t step_graph = nullptr;

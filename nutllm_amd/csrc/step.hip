@@ -18,6 +18,11 @@
 // dot: sum_k q_k s (x_k w_k) r = r * sum_k q_k s (x_k w_k) with
 // r = 1 / sqrt(mean(x^2) + 1e-5) (src/ops.cpp:111-134).
 // Every kernel returns at once when the step state says the loop ended.
+//
+// The same launches run T consecutive tokens at once (prompt chunks):
+// token t = blockIdx.y (blockIdx.z for attention) sits at position
+// *length + t, reads and writes row t of each activation buffer, and
+// attends to positions [0, *length + t]. Decode is T = 1.
 #include <algorithm>
 
 #include "kernels.hpp"
@@ -53,6 +58,9 @@ __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
     __shared__ float red[kWaves];
     if (state->done)
         return;
+    const int t = blockIdx.y;
+    hidden += size_t(t) * s.dim;
+    query += size_t(t) * s.dim;
     const int kvd = s.kv_heads * s.head_dim;
     const int row = wave_id() * R;
     const bool active = row < s.dim + 2 * kvd;
@@ -65,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
     rows_matvec<QT, R, true>(rp, sp, s.dim, hidden, norm, active, xs, red, out);
     if (!active)
         return;
-    const int pos = *length;
+    const int pos = *length + t;
     const int head = local / s.head_dim, d = local % s.head_dim;
     if (which < 2) {
 #pragma unroll
@@ -94,6 +102,8 @@ __global__ __launch_bounds__(kThreads) void residual_fast_kernel(
     extern __shared__ float xs[];
     if (state->done)
         return;
+    x += size_t(blockIdx.y) * m.cols;
+    y += size_t(blockIdx.y) * m.rows;
     const int row = wave_id() * R;
     const uint8_t *rp[R];
     const uint16_t *sp[R];
@@ -118,6 +128,8 @@ __global__ __launch_bounds__(kThreads) void gate_up_fast_kernel(
     __shared__ float red[kWaves];
     if (state->done)
         return;
+    hidden += size_t(blockIdx.y) * wg.cols;
+    act += size_t(blockIdx.y) * wg.rows;
     const int row = wave_id() * R;
     const uint8_t *rp[2 * R];
     const uint16_t *sp[2 * R];
@@ -199,7 +211,8 @@ __device__ __forceinline__ float tagged_value(uint64_t w, const uint64_t *p, uin
 // row merges them:
 //   ctx = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s,  M = max_s m_s.
 // counts[row] counts arrivals over all launches and counts[rows + row] holds
-// its value at the start of this launch (the base): a workgroup whose
+// its value at the start of this launch (the base; rows = gridDim.x, one
+// such pair of arrays per token): a workgroup whose
 // ticket is base + splits - 1 is the last, and moves the base on. The base
 // also tags this launch's words, so the merge needs no memory fence: it
 // re-reads a word until the word carries the tag.
@@ -216,9 +229,15 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
     // register file
     constexpr int PF = 2 * G * S + 8 * S <= 224 ? 4 : 2;
     constexpr int OUT = (G * HD + kThreads - 1) / kThreads;
-    const int row = blockIdx.x, split = blockIdx.y;
+    const int row = blockIdx.x, split = blockIdx.y, t = blockIdx.z;
     const int kvh = row * G / (s.heads / s.kv_heads);
-    const int n = *length + 1;
+    const int n = *length + t + 1;
+    // token t's query, context, counters and split results
+    query += size_t(t) * s.heads * HD;
+    context += size_t(t) * s.heads * HD;
+    counts += 2 * t * gridDim.x;
+    o_part += size_t(t) * s.heads * gridDim.y * (HD + 2);
+    ml_part += size_t(t) * s.heads * gridDim.y * (HD + 2);
     const int chunks = (n + kAttnChunk - 1) / kAttnChunk;
     const int want = min(int(gridDim.y), chunks);
     const int per = (chunks + want - 1) / want;
@@ -474,60 +493,60 @@ int attention_splits(const DecodeShape &s)
 
 template <int HD, int G>
 void launch_attention(const DecodeShape &s, const float *k_layer, const float *v_layer,
-                      const int *length, const StepBuffers &b, const StepState *state,
-                      hipStream_t stream)
+                      const int *length, const StepBuffers &b, int tokens,
+                      const StepState *state, hipStream_t stream)
 {
     const int splits = attention_splits(s);
     uint64_t *o_part = b.attn_part;
     uint64_t *ml_part = b.attn_part + size_t(s.heads) * splits * HD;
-    hipLaunchKernelGGL((attention_kernel<HD, G>), dim3(s.heads / G, splits),
+    hipLaunchKernelGGL((attention_kernel<HD, G>), dim3(s.heads / G, splits, tokens),
                        dim3(kThreads), 0, stream, s, b.query, k_layer, v_layer, length,
                        o_part, ml_part, b.attn_count, b.context, state);
 }
 
 template <int HD>
 void launch_attention_g(const DecodeShape &s, const float *k_layer, const float *v_layer,
-                        const int *length, const StepBuffers &b, const StepState *state,
-                        hipStream_t stream)
+                        const int *length, const StepBuffers &b, int tokens,
+                        const StepState *state, hipStream_t stream)
 {
     if (attention_group(s) == 2)
-        launch_attention<HD, 2>(s, k_layer, v_layer, length, b, state, stream);
+        launch_attention<HD, 2>(s, k_layer, v_layer, length, b, tokens, state, stream);
     else
-        launch_attention<HD, 1>(s, k_layer, v_layer, length, b, state, stream);
+        launch_attention<HD, 1>(s, k_layer, v_layer, length, b, tokens, state, stream);
 }
 
 template <int QT, int HD>
 void launch_layer_fast_t(const DecodeShape &s, const LayerView &w,
                          const float2 *rope, const int *length, float *k_layer,
-                         float *v_layer, const StepBuffers &b,
+                         float *v_layer, const StepBuffers &b, int tokens,
                          const StepState *state, hipStream_t stream)
 {
     const int kvd = s.kv_heads * s.head_dim;
     const size_t x_dim = staged_x_bytes<QT>(s.dim), x_ffn = staged_x_bytes<QT>(s.ffn_dim);
-    // four rows per wave where that still gives every CU a workgroup
     const int qkv_rows = s.dim + 2 * kvd;
+    // four rows per wave where that still gives every CU a workgroup
     if (qkv_rows >= 8192 && s.dim % 4 == 0 && kvd % 4 == 0)
-        hipLaunchKernelGGL((qkv_fast_kernel<QT, 4>), dim3(blocks_for_rows(qkv_rows, 4)),
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 4>), dim3(blocks_for_rows(qkv_rows, 4), tokens),
                            dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
                            w.query, w.key, w.value, rope, length, k_layer, v_layer,
                            b.query, state);
     else
-        hipLaunchKernelGGL((qkv_fast_kernel<QT, 2>), dim3(blocks_for_rows(qkv_rows, 2)),
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 2>), dim3(blocks_for_rows(qkv_rows, 2), tokens),
                            dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
                            w.query, w.key, w.value, rope, length, k_layer, v_layer,
                            b.query, state);
-    launch_attention_g<HD>(s, k_layer, v_layer, length, b, state, stream);
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2)),
+    launch_attention_g<HD>(s, k_layer, v_layer, length, b, tokens, state, stream);
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2), tokens),
                        dim3(kThreads), x_dim, stream, w.output, b.context, b.hidden, state);
     if (s.ffn_dim >= 8192)
-        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4>), dim3(blocks_for_rows(s.ffn_dim, 4)),
-                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate,
-                           w.up, b.act, state);
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4>),
+                           dim3(blocks_for_rows(s.ffn_dim, 4), tokens), dim3(kThreads), x_dim,
+                           stream, b.hidden, w.ffn_norm, w.gate, w.up, b.act, state);
     else
-        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.ffn_dim, 2)),
-                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate,
-                           w.up, b.act, state);
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2)),
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 2>),
+                           dim3(blocks_for_rows(s.ffn_dim, 2), tokens), dim3(kThreads), x_dim,
+                           stream, b.hidden, w.ffn_norm, w.gate, w.up, b.act, state);
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2), tokens),
                        dim3(kThreads), x_ffn, stream, w.down, b.act, b.hidden, state);
     check_launch("decode step");
 }
@@ -553,22 +572,24 @@ bool step_fast_supported(const DecodeShape &s, const LayerView &w)
 
 size_t step_attn_part_words(const DecodeShape &s)
 {
-    return size_t(s.heads) * attention_splits(s) * (size_t(s.head_dim) + 2);
+    return size_t(kStepTokensMax) * s.heads * attention_splits(s) * (size_t(s.head_dim) + 2);
 }
 
 void launch_layer_fast(const DecodeShape &s, const LayerView &w,
                        const float2 *rope, const int *length, float *k_layer,
-                       float *v_layer, const StepBuffers &b,
+                       float *v_layer, const StepBuffers &b, int tokens,
                        const StepState *state, hipStream_t stream)
 {
+    require(tokens >= 1 && tokens <= kStepTokensMax, NUT_EINVAL,
+            "decode step: token count out of range");
     if (w.query.type == 1)
         s.head_dim == 128
-            ? launch_layer_fast_t<1, 128>(s, w, rope, length, k_layer, v_layer, b, state, stream)
-            : launch_layer_fast_t<1, 64>(s, w, rope, length, k_layer, v_layer, b, state, stream);
+            ? launch_layer_fast_t<1, 128>(s, w, rope, length, k_layer, v_layer, b, tokens, state, stream)
+            : launch_layer_fast_t<1, 64>(s, w, rope, length, k_layer, v_layer, b, tokens, state, stream);
     else
         s.head_dim == 128
-            ? launch_layer_fast_t<0, 128>(s, w, rope, length, k_layer, v_layer, b, state, stream)
-            : launch_layer_fast_t<0, 64>(s, w, rope, length, k_layer, v_layer, b, state, stream);
+            ? launch_layer_fast_t<0, 128>(s, w, rope, length, k_layer, v_layer, b, tokens, state, stream)
+            : launch_layer_fast_t<0, 64>(s, w, rope, length, k_layer, v_layer, b, tokens, state, stream);
 }
 
 } // namespace nut

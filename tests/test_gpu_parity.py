@@ -291,13 +291,36 @@ def test_tiny_matches_reference_golden(gpu, qtype, tag):
     dev.close()
 
 
+@pytest.mark.parametrize("prompt_len", [2, 5, 15])
+def test_tinyllama_int4_prefill_step_chunk(gpu, tinyllama_int4, prompt_len):
+    """Prompts below the GEMM threshold run as one chunk of consecutive
+    tokens through the step kernels (each launch covers every token; the
+    arithmetic per token is the decode step's). Hidden state and K/V rows
+    within rel-L2 1e-5 of the oracle's per-token prefill."""
+    model, _, _, dev = tinyllama_int4
+    prompt = gpu.synth_tokens(17, model.config.vocab_size, prompt_len)
+    cache = gpu.KVCache(model.config)
+    dev.set_path(0)
+    h = dev.prefill(cache, prompt)
+    om = O.oracle_model(model)
+    assert rel_l2(h, om.prefill(prompt)) <= TOL
+    for layer in (0, model.config.layers - 1):
+        for kvh in range(model.config.kv_heads):
+            for p in sorted({0, prompt_len // 2, prompt_len - 1}):
+                k, v = cache.key_value(layer, kvh, p)
+                rk, rv = om.kv_row(layer, kvh, p)
+                assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+    # the next decode step continues from the chunked prefill
+    assert rel_l2(dev.decode(cache, 7), om.decode(7)) <= TOL
+
+
 PREFILL_TOL = 2e-3  # rel-L2, batched (GEMM) prefill
 
 
 @pytest.mark.parametrize("prompt_len", [40, 130])
 def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
     """Prompts of 16+ tokens run as a batch (MFMA GEMMs, causal attention).
-    Hidden state and K/V rows within rel-L2 2e-3 of the per-token path
+    Hidden state and K/V rows within rel-L2 2e-3 of the fp32 step arithmetic
     (oracle for 40 tokens, the device step kernels for 130), and the greedy
     ids that follow the prefill identical to the oracle's."""
     model, _, _, dev = tinyllama_int4
@@ -357,9 +380,9 @@ def test_step_kernels_long_context(gpu, shape, qtype):
     """Step kernels against the oracle at a 1100-token context: RMSNorm
     folded into the Q/K/V and gate/up matvecs (non-unit norm weights), and
     attention split over 35 chunks of 32 positions whose splits are merged
-    by the last workgroup of each KV head. Hidden state after the per-token
-    prefill, K/V rows and each decode step of the greedy continuation
-    (rel-L2 1e-5); 8 greedy ids identical."""
+    by the last workgroup of each KV head. Hidden state after the prefill
+    (74 chunks of up to 15 consecutive tokens), K/V rows and each decode
+    step of the greedy continuation (rel-L2 1e-5); 8 greedy ids identical."""
     O.orc().orc_set_threads(16)
     model = W.build(shape, qtype, 5)
     c = model.config
