@@ -215,11 +215,13 @@ int nut_model_set_path(nut_model *m, int path);
 /* Phase timeline of the cooperative token kernel, for profiling (no
  * reference counterpart). mode 0 records nothing, 1 workgroup 0, 2 every
  * workgroup of the grid (256): each stamps the device's constant 100 MHz
- * clock at each phase boundary; per decode iteration 2 + 9 * layers
+ * clock at each phase boundary; per decode iteration 2 + 13 * layers
  * entries: iteration start, token known, then per layer the times its QKV
- * input is staged, QKV published, attention input staged, attention done,
- * Wo published, FFN input staged, gate/up published, down input staged and
- * down published. Entries are [workgroup][max_seq iterations][marks].
+ * input is staged, QKV published, Wo/K/V DMA issued, attention input
+ * staged, attention done, Wo published, gate/up DMA issued, FFN input
+ * staged, gate/up published, down DMA issued, down input staged, down
+ * published and next QKV DMA issued. Entries are
+ * [workgroup][max_seq iterations][marks].
  * nut_model_timeline copies up to capacity entries of the last launch's
  * timeline. */
 int nut_model_record_timeline(nut_model *m, int mode);

@@ -760,7 +760,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
             }
             stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
-            mark(it, 2 + 9 * l);
+            mark(it, 2 + 13 * l);
             {
                 XRegs<G::CPL_DIM> x;
                 load_x(x, xs, xsum, G::BLK_DIM);
@@ -799,6 +799,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // K/V rows of earlier positions stream into LDS while the q/k/v
             // exchange completes.
             __syncthreads();
+            mark(it, 3 + 13 * l);
             const int n = pos + 1;
             float *vst = kst + G::KVH * n * G::KROW;
             if (pos > 0)
@@ -809,7 +810,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                                     vc + size_t(kvh) * a.max_seq * G::HD, pos);
                 }
             stage_wo(l);
-            mark(it, 3 + 9 * l);
+            mark(it, 4 + 13 * l);
 
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
@@ -823,7 +824,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
 
             __syncthreads();
-            mark(it, 4 + 9 * l);
+            mark(it, 5 + 13 * l);
             {
                 // Wave w: query heads 4w..4w+3, all of kv head 4w / GROUP.
                 // Lane (hh = lane / 16, r = lane % 16): scores of head hh at
@@ -899,7 +900,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
             __syncthreads();
             block_sums(xs, xsum, G::DIM);
-            mark(it, 5 + 9 * l);
+            mark(it, 6 + 13 * l);
             for (int r = wave; r < wo_e - wo_b; r += kWaves) {
                 const uint8_t *d;
                 const uint16_t *s;
@@ -912,14 +913,15 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // every wave is past attention (region 1) and past its reads of
             // h_raw, which phase C's take overwrites
             __syncthreads();
+            mark(it, 7 + 13 * l);
             stage_gu(l);
-            mark(it, 6 + 9 * l);
+            mark(it, 8 + 13 * l);
 
             // ------------------------------------------ phase C: gate/up --
             nw.load(norm(l, true));
             sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
             stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
-            mark(it, 7 + 9 * l);
+            mark(it, 9 + 13 * l);
             {
                 XRegs<G::CPL_DIM> x;
                 load_x(x, xs, xsum, G::BLK_DIM);
@@ -936,13 +938,14 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
             tag++;
             __syncthreads();
+            mark(it, 10 + 13 * l);
             stage_down(l);
-            mark(it, 8 + 9 * l);
+            mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
             take<G::FFN, true>(a.x_act, xs, tag - 1, error);
             block_sums(xs, xsum, G::FFN);
-            mark(it, 9 + 9 * l);
+            mark(it, 12 + 13 * l);
             {
                 const bool last = l + 1 == a.layer_count;
                 for (int r = wave; r < dn_e - dn_b; r += kWaves) {
@@ -958,12 +961,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     }
                 }
                 __syncthreads();
+                mark(it, 13 + 13 * l);
                 if (!last)
                     stage_qkv(l + 1);
             }
             hidden_tag = tag;
             tag++;
-            mark(it, 10 + 9 * l);
+            mark(it, 14 + 13 * l);
         }
         if (wg_failed(error, misc + 8))
             break;

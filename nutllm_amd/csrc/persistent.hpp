@@ -41,11 +41,12 @@ struct TokenArgs {
 };
 
 // Timeline entries per iteration: iteration start, token known, then per
-// layer: A input staged, A published, B input, attention done, B published,
-// C input, C published, D input, D published.
+// layer, for each of the phases A, B, C, D: input staged, outputs published
+// (every wave past its publishes), next weights issued to LDS DMA; phase B
+// also marks attention done after its input.
 __host__ __device__ inline int marks_per_iteration(int layers)
 {
-    return 2 + 9 * layers;
+    return 2 + 13 * layers;
 }
 
 // Longest context (positions) the kernel's fused attention phase handles
