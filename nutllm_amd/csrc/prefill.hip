@@ -5,10 +5,10 @@
 //   rmsnorm rows -> Q/K/V GEMMs -> RoPE + KV-cache store -> causal attention
 //   -> Wo GEMM (+ residual) -> rmsnorm rows -> gate/up GEMMs -> silu * up
 //   -> W2 GEMM (+ residual)
-// The quantised GEMMs dequantise each 32-weight block exactly into LDS as
-// fp32 (q * fp16 scale is exact in fp32) and run v_mfma_f32_16x16x4f32, so
-// every product is exact and only the summation order differs from the
-// per-token path.
+// The quantised GEMMs run on f16 MFMA with the weight codes exact in f16,
+// the activations split into two f16 limbs and the block scales applied
+// in fp32 per 32-wide block; attention runs on fp32 MFMA. The hidden state
+// stays within about 1e-5 of the per-token path (fp32 throughout).
 #include "prefill.hpp"
 #include "runtime.hpp"
 
@@ -91,117 +91,149 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
     }
 }
 
-// --------------------------------------------------- quantised GEMM --
+// ------------------------------------- quantised GEMM on f16 MFMA --
 
-// C[t][n] (= or +=) sum_k X[t][k] W[n][k]; W quantised (block 32 along k,
-// k % 32 == 0). A workgroup owns 64 tokens x 64 outputs; four waves of
-// 2 x 2 MFMA tiles. Per 32-wide k slice: X (64 x 32) and the W rows' block
-// (64 x 32, dequantised) go to LDS; the next slice's raw bytes are loaded
-// into registers during the MFMAs.
-constexpr int BM = 64, BN = 64, BK = 32;
+// C[t][n] (= or +=) sum_k X[t][k] W[n][k], W quantised (block 32 along k,
+// k % 32 == 0), on v_mfma_f32_16x16x32_f16, whose K = 32 is one quant
+// block:
+//   * W codes q (INT4 -8..7, INT8 -128..127) are exact in f16;
+//   * X is split into two f16 limbs, hi = f16(x) and lo = f16(x - hi), so
+//     hi + lo carries x to about 2^-22 relative (f16 subnormals aside);
+//   * every product of two f16 values is exact in the fp32 accumulator;
+//   * per block, D = A_hi B + A_lo B, then acc += s_n D with the block's
+//     fp16 scale s_n (one column n per lane in the D layout).
+// A workgroup owns 128 tokens x 128 outputs; four waves of 4 x 4 MFMA
+// tiles (64 x 64 each). Per 32-wide k slice the limbs of X and the W codes
+// go to LDS (double-buffered), and the next slice is loaded into registers
+// during the MFMAs. Lane layout (measured): A[i][k] in lane i % 16 + 16 g
+// holding k = 8 g .. 8 g + 7; B[k][n] likewise with n = lane % 16;
+// D[i][n] in lane n + 16 (i / 4), element i % 4.
+constexpr int FM = 128, FN = 128, FK = 32;
+constexpr int FROW = FK + 8; // f16 per LDS row (16-byte pad)
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 template <int QT, bool ADD>
-__global__ __launch_bounds__(kThreads) void qgemm_kernel(
-    const float *__restrict__ x, int t_count, QMat w, float *__restrict__ c,
-    int ldc)
+__global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
+    const float *__restrict__ x, int t_count, QMat w, float *__restrict__ c, int ldc)
 {
-    __shared__ float xs[BK][BM + 4]; // X slice, transposed: xs[k][t]
-    __shared__ float ws[BK][BN + 4]; // W slice, dequantised: ws[k][n]
+    __shared__ __attribute__((aligned(16))) _Float16 xh[2][FM][FROW];
+    __shared__ __attribute__((aligned(16))) _Float16 xl[2][FM][FROW];
+    __shared__ __attribute__((aligned(16))) _Float16 wq[2][FN][FROW];
+    __shared__ float wsc[2][FN];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
-    const int k = w.cols, n_count = w.rows;
-    // X loader: rows xr, xr + 32; k columns xc .. xc + 3
-    const int xr = tid >> 3, xc = (tid & 7) * 4;
-    // W loader: row wn (64 rows, 4 threads each), weights 8 * wp .. + 7
-    const int wn = tid >> 2, wp = tid & 3;
-    const int wrow = min(n0 + wn, n_count - 1);
+    const int t0 = blockIdx.y * FM, n0 = blockIdx.x * FN;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int k = w.cols, n_count = w.rows, blocks = k / FK;
+    // loader: row r = tid / 2 of both tiles, 16 consecutive k from 16 h
+    const int r = tid >> 1, h = tid & 1;
+    const int xrow = t0 + r;
+    const float *xp = x + size_t(min(xrow, t_count - 1)) * k + 16 * h;
+    const int wrow = min(n0 + r, n_count - 1);
     constexpr int RB_DIV = QT == 1 ? 2 : 1;
-    const uint8_t *wdata = w.data + size_t(wrow) * (k / RB_DIV);
-    const uint16_t *wsc = w.scales + size_t(wrow) * (k / 32);
-    float4 rx[2];
-    uint2 rw; // 8 weights: INT4 uses rw.x only
-    uint16_t rs;
-    auto load = [&](int k0) {
+    const uint8_t *wp = w.data + size_t(wrow) * (k / RB_DIV) + (QT == 1 ? 8 : 16) * h;
+    const uint16_t *sp = w.scales + size_t(wrow) * blocks;
+    float4 rx[4];
+    uint4 rw; // INT4 uses .x, .y (16 nibbles); INT8 all (16 bytes)
+    uint16_t rs = 0;
+    auto load = [&](int kb) {
+        const float4 *src = reinterpret_cast<const float4 *>(xp + kb * FK);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int t = t0 + xr + 32 * h;
-            rx[h] = t < t_count
-                        ? *reinterpret_cast<const float4 *>(x + size_t(t) * k + k0 + xc)
-                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        for (int j = 0; j < 4; j++)
+            rx[j] = xrow < t_count ? src[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (QT == 1) {
-            rw.x = *reinterpret_cast<const uint32_t *>(wdata + k0 / 2 + 4 * wp);
-            rw.y = 0;
+            const uint2 v = *reinterpret_cast<const uint2 *>(wp + kb * (FK / 2));
+            rw = make_uint4(v.x, v.y, 0u, 0u);
         } else {
-            rw = *reinterpret_cast<const uint2 *>(wdata + k0 + 8 * wp);
+            rw = *reinterpret_cast<const uint4 *>(wp + kb * FK);
         }
-        rs = wsc[k0 / 32];
+        if (h == 0)
+            rs = sp[kb];
     };
-    auto store = [&]() {
+    auto stage = [&](int buf) {
+        half8 hi[2], lo[2];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int r = xr + 32 * h;
-            xs[xc][r] = rx[h].x;
-            xs[xc + 1][r] = rx[h].y;
-            xs[xc + 2][r] = rx[h].z;
-            xs[xc + 3][r] = rx[h].w;
-        }
-        const float s = half_bits_to_float(rs);
+        for (int j = 0; j < 4; j++) {
+            const float v[4] = {rx[j].x, rx[j].y, rx[j].z, rx[j].w};
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            int q;
-            if (QT == 1) {
-                const uint32_t nib = (rw.x >> (4 * e)) & 0xfu;
-                q = int(nib) - (nib >= 8 ? 16 : 0);
-            } else {
-                const uint32_t word = e < 4 ? rw.x : rw.y;
-                q = int(int8_t((word >> (8 * (e & 3))) & 0xffu));
+            for (int e = 0; e < 4; e++) {
+                const _Float16 a = (_Float16)v[e];
+                hi[j >> 1][4 * (j & 1) + e] = a;
+                lo[j >> 1][4 * (j & 1) + e] = (_Float16)(v[e] - (float)a);
             }
-            ws[8 * wp + e][wn] = float(q) * s;
         }
+        half8 q[2];
+        const uint32_t words[4] = {rw.x, rw.y, rw.z, rw.w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            int code;
+            if (QT == 1) {
+                const uint32_t nib = (words[e >> 3] >> (4 * (e & 7))) & 0xfu;
+                code = int(nib) - (nib >= 8 ? 16 : 0);
+            } else {
+                code = int(int8_t((words[e >> 2] >> (8 * (e & 3))) & 0xffu));
+            }
+            q[e >> 3][e & 7] = (_Float16)code;
+        }
+        *reinterpret_cast<half8 *>(&xh[buf][r][16 * h]) = hi[0];
+        *reinterpret_cast<half8 *>(&xh[buf][r][16 * h + 8]) = hi[1];
+        *reinterpret_cast<half8 *>(&xl[buf][r][16 * h]) = lo[0];
+        *reinterpret_cast<half8 *>(&xl[buf][r][16 * h + 8]) = lo[1];
+        *reinterpret_cast<half8 *>(&wq[buf][r][16 * h]) = q[0];
+        *reinterpret_cast<half8 *>(&wq[buf][r][16 * h + 8]) = q[1];
+        if (h == 0)
+            wsc[buf][r] = half_bits_to_float(rs);
     };
-    floatx4 acc[2][2];
+    floatx4 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     load(0);
-    for (int k0 = 0; k0 < k; k0 += BK) {
-        store();
-        __syncthreads();
-        if (k0 + BK < k)
-            load(k0 + BK);
+    stage(0);
+    __syncthreads();
+    const int g = lane >> 4, li = lane & 15;
+    for (int kb = 0; kb < blocks; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < blocks)
+            load(kb + 1);
+        half8 ah[4], al[4], b[4];
+        float sc[4];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 4) {
-            const int ka = kk + (lane >> 4);
-            float af[2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                af[i] = xs[ka][wr + i * 16 + (lane & 15)];
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                bf[j] = ws[ka][wc + j * 16 + (lane & 15)];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; i++) {
+            ah[i] = *reinterpret_cast<const half8 *>(&xh[buf][wm + 16 * i + li][8 * g]);
+            al[i] = *reinterpret_cast<const half8 *>(&xl[buf][wm + 16 * i + li][8 * g]);
         }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            b[j] = *reinterpret_cast<const half8 *>(&wq[buf][wn + 16 * j + li][8 * g]);
+            sc[j] = wsc[buf][wn + 16 * j + li];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    ah[i], b[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], d, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[i][j][v] = fmaf(sc[j], d[v], acc[i][j][v]);
+            }
+        if (kb + 1 < blocks)
+            stage(buf ^ 1);
         __syncthreads();
     }
-    // D layout: lane holds rows 4 * (lane / 16) + v, column lane % 16.
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int t = t0 + wr + i * 16 + 4 * (lane >> 4) + v;
-                const int n = n0 + wc + j * 16 + (lane & 15);
+                const int t = t0 + wm + 16 * i + 4 * g + v;
+                const int n = n0 + wn + 16 * j + li;
                 if (t < t_count && n < n_count) {
                     float *p = c + size_t(t) * ldc + n;
                     *p = ADD ? *p + acc[i][j][v] : acc[i][j][v];
@@ -211,112 +243,134 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(
 
 // ------------------------------------------------ causal attention --
 
-// One workgroup per (64-query tile, head): queries t0 .. t0 + 63 at
-// positions start + t attend to cache positions 0 .. start + t. Key tiles
-// of 64 positions stream through LDS; scores, the online softmax and the
-// context accumulate in fp32. Thread (i = tid / 4, part = tid % 4) owns
-// query row i: scores of keys 16 part .. 16 part + 15 of each tile and
-// context columns part * HD / 4 .. (part + 1) * HD / 4 - 1.
+// Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
+// start + t attend to cache positions 0 .. start + t, in 64-key tiles.
 constexpr int AQ = 64, AK = 64;
 
+// On v_mfma_f32_16x16x4f32 (fp32 operands, as the reference's
+// arithmetic): one workgroup per (64-query tile, head);
+// wave w owns queries 16 w .. 16 w + 15. Per 64-key tile (K and V in LDS):
+// S = Q K^T as 4 x (HD / 4) MFMAs with Q in registers, the online softmax
+// on S in registers (a query row lives in one 16-lane DPP row), P through
+// LDS into the A layout, then O += P V as (HD / 16) x 16 MFMAs. Lane
+// layouts of the 16x16x4 MFMA: A[i][k] in lane i + 16 k, B[k][n] in lane
+// n + 16 k, D[i][n] in lane n + 16 (i / 4), element i % 4.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_prefill_kernel(
+__global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
     const float *q, const float *k_cache, const float *v_cache, float *ctx,
     int t_count, int heads, int kv_heads, int max_seq, int start, float scale)
 {
-    __shared__ float qs[AQ][HD + 4];
-    __shared__ float kt[HD][AK + 4]; // K tile transposed: kt[d][j]
-    __shared__ float vs[AK][HD + 4];
-    __shared__ float ps[AQ][AK + 4];
-    const int tid = threadIdx.x;
+    constexpr int KP = HD + 4, VP = HD + 16, PP = AK + 4;
+    __shared__ float ks[AK][KP];
+    __shared__ float vs[AK][VP];
+    __shared__ float ps[4][16][PP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
     const int head = blockIdx.y, g = head / (heads / kv_heads);
     const int t0 = blockIdx.x * AQ;
     const int dim = heads * HD;
-    const int i = tid >> 2, part = tid & 3;
-    for (int e = tid; e < AQ * HD; e += kThreads) {
-        const int r = e / HD, d = e % HD;
-        qs[r][d] = t0 + r < t_count ? q[size_t(t0 + r) * dim + head * HD + d] : 0.0f;
+    // Q fragments of this wave's rows: A[i = li][k = 4 s + lg]
+    float qa[HD / 4];
+    {
+        const int t = t0 + 16 * wave + li;
+        const float *qr = q + size_t(min(t, t_count - 1)) * dim + head * HD;
+#pragma unroll
+        for (int st = 0; st < HD / 4; st++)
+            qa[st] = t < t_count ? qr[4 * st + lg] : 0.0f;
     }
     const float *kg = k_cache + size_t(g) * max_seq * HD;
     const float *vg = v_cache + size_t(g) * max_seq * HD;
-    const int my_pos = start + t0 + i; // position of query row i
     const int last = min(start + t0 + AQ - 1, start + t_count - 1);
-    constexpr int OC = HD / 4; // context columns per thread
-    float m = -INFINITY, l = 0.0f;
-    float o[OC];
+    // rows of this lane: r = 4 lg + v (v < 4) of the wave's 16
+    int qpos[4];
 #pragma unroll
-    for (int d = 0; d < OC; d++)
-        o[d] = 0.0f;
+    for (int v = 0; v < 4; v++)
+        qpos[v] = start + t0 + 16 * wave + 4 * lg + v;
+    float m[4], l[4];
+    floatx4 o[HD / 16];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        m[v] = -INFINITY;
+        l[v] = 0.0f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; dt++)
+        o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int p0 = 0; p0 <= last; p0 += AK) {
         __syncthreads(); // previous tile's readers are done
-        for (int e = tid; e < AK * HD; e += kThreads) {
-            const int j = e / HD, d = e % HD;
+        for (int e = tid; e < AK * HD / 4; e += kThreads) {
+            const int j = e / (HD / 4), d4 = e % (HD / 4);
             const bool in = p0 + j <= last;
-            kt[d][j] = in ? kg[size_t(p0 + j) * HD + d] : 0.0f;
-            vs[j][d] = in ? vg[size_t(p0 + j) * HD + d] : 0.0f;
+            const float4 kv = in ? reinterpret_cast<const float4 *>(kg + size_t(p0 + j) * HD)[d4]
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 vv = in ? reinterpret_cast<const float4 *>(vg + size_t(p0 + j) * HD)[d4]
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            *reinterpret_cast<float4 *>(&ks[j][4 * d4]) = kv;
+            *reinterpret_cast<float4 *>(&vs[j][4 * d4]) = vv;
         }
         __syncthreads();
-        float s[16];
+        // S tiles: keys 16 nt + li, rows 4 lg + v
+        floatx4 sc[4];
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++)
-            s[jj] = 0.0f;
-        for (int d = 0; d < HD; d++) {
-            const float qd = qs[i][d];
+        for (int nt = 0; nt < 4; nt++) {
+            sc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int jj = 0; jj < 16; jj += 4) {
-                const float4 kk = *reinterpret_cast<const float4 *>(&kt[d][16 * part + jj]);
-                s[jj] = fmaf(qd, kk.x, s[jj]);
-                s[jj + 1] = fmaf(qd, kk.y, s[jj + 1]);
-                s[jj + 2] = fmaf(qd, kk.z, s[jj + 2]);
-                s[jj + 3] = fmaf(qd, kk.w, s[jj + 3]);
+            for (int st = 0; st < HD / 4; st++)
+                sc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    qa[st], ks[16 * nt + li][4 * st + lg], sc[nt], 0, 0, 0);
+        }
+        float corr[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const int kpos = p0 + 16 * nt + li;
+                const float x = kpos <= qpos[v] ? sc[nt][v] * scale : -INFINITY;
+                sc[nt][v] = x;
+                tmax = fmaxf(tmax, x);
             }
-        }
-        float tile_max = -INFINITY;
+            tmax = row16_max(tmax);
+            const float mn = fmaxf(m[v], tmax);
+            // rows past t_count (and fully masked tiles) keep m = -inf
+            corr[v] = mn == -INFINITY ? 1.0f : expf(m[v] - mn);
+            float sum = 0.0f;
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++) {
-            const int pos = p0 + 16 * part + jj;
-            s[jj] = pos <= my_pos ? s[jj] * scale : -INFINITY;
-            tile_max = fmaxf(tile_max, s[jj]);
-        }
-        // the four threads of row i share max and sum (quad DPP)
-        tile_max = fmaxf(tile_max, dpp<kDppQuadSwap1>(tile_max, -INFINITY));
-        tile_max = fmaxf(tile_max, dpp<kDppQuadSwap2>(tile_max, -INFINITY));
-        const float m_new = fmaxf(m, tile_max);
-        // rows past t_count (and fully masked tiles) keep m = -inf
-        const float correction = m_new == -INFINITY ? 1.0f : expf(m - m_new);
-        float sum = 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < 16; jj++) {
-            const float e = s[jj] == -INFINITY ? 0.0f : expf(s[jj] - m_new);
-            ps[i][16 * part + jj] = e;
-            sum += e;
-        }
-        sum += dpp<kDppQuadSwap1>(sum, 0.0f);
-        sum += dpp<kDppQuadSwap2>(sum, 0.0f);
-        l = l * correction + sum;
-        m = m_new;
-#pragma unroll
-        for (int d = 0; d < OC; d++)
-            o[d] *= correction;
-        __syncthreads(); // ps complete
-        for (int j = 0; j < AK; j++) {
-            const float pj = ps[i][j];
-#pragma unroll
-            for (int d = 0; d < OC; d += 4) {
-                const float4 vv = *reinterpret_cast<const float4 *>(&vs[j][OC * part + d]);
-                o[d] = fmaf(pj, vv.x, o[d]);
-                o[d + 1] = fmaf(pj, vv.y, o[d + 1]);
-                o[d + 2] = fmaf(pj, vv.z, o[d + 2]);
-                o[d + 3] = fmaf(pj, vv.w, o[d + 3]);
+            for (int nt = 0; nt < 4; nt++) {
+                const float e = sc[nt][v] == -INFINITY ? 0.0f : expf(sc[nt][v] - mn);
+                ps[wave][4 * lg + v][16 * nt + li] = e;
+                sum += e;
             }
+            l[v] = l[v] * corr[v] + row16_sum(sum);
+            m[v] = mn;
+        }
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; dt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                o[dt][v] *= corr[v];
+        // ps rows of this wave are written by this wave only
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): LDS writes done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int st = 0; st < AK / 4; st++) {
+            const float pa = ps[wave][li][4 * st + lg];
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                    pa, vs[4 * st + lg][16 * dt + li], o[dt], 0, 0, 0);
         }
     }
-    if (t0 + i < t_count) {
-        const float inv = 1.0f / l;
-        float *out = ctx + size_t(t0 + i) * dim + head * HD + OC * part;
 #pragma unroll
-        for (int d = 0; d < OC; d++)
-            out[d] = o[d] * inv;
+    for (int v = 0; v < 4; v++) {
+        const int t = t0 + 16 * wave + 4 * lg + v;
+        if (t < t_count) {
+            const float inv = 1.0f / l[v];
+            float *out = ctx + size_t(t) * dim + head * HD;
+#pragma unroll
+            for (int dt = 0; dt < HD / 16; dt++)
+                out[16 * dt + li] = o[dt][v] * inv;
+        }
     }
 }
 
@@ -324,12 +378,12 @@ template <int QT>
 void launch_qgemm(const float *x, int t_count, const QMat &w, float *c, int ldc,
                   bool add, hipStream_t stream)
 {
-    const dim3 grid((w.rows + BN - 1) / BN, (t_count + BM - 1) / BM);
+    const dim3 grid((w.rows + FN - 1) / FN, (t_count + FM - 1) / FM);
     if (add)
-        hipLaunchKernelGGL((qgemm_kernel<QT, true>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true>), grid, dim3(kThreads), 0,
                            stream, x, t_count, w, c, ldc);
     else
-        hipLaunchKernelGGL((qgemm_kernel<QT, false>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false>), grid, dim3(kThreads), 0,
                            stream, x, t_count, w, c, ldc);
 }
 
@@ -389,11 +443,11 @@ void launch_attention_prefill(const float *q, const float *k_cache,
 {
     const dim3 grid((t_count + AQ - 1) / AQ, s.heads);
     if (s.head_dim == 128)
-        hipLaunchKernelGGL(attention_prefill_kernel<128>, grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL(attention_prefill_mfma<128>, grid, dim3(kThreads), 0,
                            stream, q, k_cache, v_cache, ctx, t_count, s.heads,
                            s.kv_heads, s.max_seq, start, s.attn_scale);
     else
-        hipLaunchKernelGGL(attention_prefill_kernel<64>, grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL(attention_prefill_mfma<64>, grid, dim3(kThreads), 0,
                            stream, q, k_cache, v_cache, ctx, t_count, s.heads,
                            s.kv_heads, s.max_seq, start, s.attn_scale);
     check_launch("prefill attention");

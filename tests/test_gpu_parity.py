@@ -352,6 +352,42 @@ def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
         assert ids == ref_ids
 
 
+@pytest.mark.parametrize("shape,qtype", [("step_mha128", 1), ("step_gqa4", 0)],
+                         ids=["mha128-int4", "gqa4-int8"])
+def test_prefill_gemm_other_heads(gpu, shape, qtype):
+    """Batched prefill of 200 tokens at head_dim 128 with one query head
+    per KV head, and at head_dim 64 with four, non-unit norm weights:
+    hidden state and K/V rows within rel-L2 2e-3 of the oracle."""
+    O.orc().orc_set_threads(16)
+    model = W.build(shape, qtype, 6)
+    c = model.config
+    rng = np.random.default_rng(9)
+    norms = [tuple((1.0 + 0.25 * rng.standard_normal(c.dim)).astype(np.float32)
+                   for _ in range(2)) for _ in range(c.layers)]
+    dev = gpu.DeviceModel(c, qtype)
+    dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
+    for i, mats in enumerate(model.layers):
+        dev.set_layer(i, mats, norms[i][0], norms[i][1])
+    cfg = {n: getattr(c, n) for n, _ in O.OrcConfig._fields_}
+    om = O.OracleModel(cfg, qtype, model.embeddings, model.final_norm,
+                       model.lm_head, model.layers, norms)
+    prompt = gpu.synth_tokens(23, c.vocab_size, 200)
+    try:
+        cache = gpu.KVCache(c)
+        h = dev.prefill(cache, prompt)
+        err = rel_l2(h, om.prefill(prompt))
+        print(f"{shape}: prefill hidden rel-L2 {err:.2e}", flush=True)
+        assert err <= PREFILL_TOL
+        for layer in range(c.layers):
+            for kvh in range(c.kv_heads):
+                for p in (0, 99, 199):
+                    k, v = cache.key_value(layer, kvh, p)
+                    rk, rv = om.kv_row(layer, kvh, p)
+                    assert rel_l2(k, rk) <= PREFILL_TOL and rel_l2(v, rv) <= PREFILL_TOL
+    finally:
+        dev.close()
+
+
 def test_tinyllama_int4_graph_replays_match_eager(gpu, tinyllama_int4):
     """A 60-token prompt is past the token kernel's fused attention, so
     generation replays a captured graph of one greedy iteration per token.
