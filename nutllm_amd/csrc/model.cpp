@@ -215,9 +215,12 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         m.pf_u.allocate(rows * c.ffn_dim * sizeof(float));
     }
     const int t = int(count);
-    float *h = m.pf_h.as<float>(), *x = m.pf_x.as<float>();
+    // GEMM inputs as f16 limbs (hi rows, then lo rows): the normalised x and
+    // the SwiGLU activations in pf_x, the attention context in pf_ctx
+    float *h = m.pf_h.as<float>();
+    _Float16 *xh = m.pf_x.as<_Float16>(), *ch = m.pf_ctx.as<_Float16>();
     float *q = m.pf_q.as<float>(), *k = m.pf_k.as<float>(), *v = m.pf_v.as<float>();
-    float *ctx = m.pf_ctx.as<float>(), *g = m.pf_g.as<float>(), *u = m.pf_u.as<float>();
+    float *g = m.pf_g.as<float>(), *u = m.pf_u.as<float>();
     launch_embed_rows(m.embeddings.as<float>(), m.prompt.as<int>(), h, t, s.dim,
                       m.stream);
     const size_t layer_elems = kv.layer_elements();
@@ -225,18 +228,28 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         const LayerView &w = m.layers[l].view;
         float *kc = kv.keys.as<float>() + l * layer_elems;
         float *vc = kv.values.as<float>() + l * layer_elems;
-        launch_rmsnorm_rows(h, w.attention_norm, x, t, s.dim, m.stream);
-        launch_qgemm_rows(x, t, w.query, q, s.dim, false, m.stream);
-        launch_qgemm_rows(x, t, w.key, k, int(kvd), false, m.stream);
-        launch_qgemm_rows(x, t, w.value, v, int(kvd), false, m.stream);
+        const QMat *qkv_w[3] = {&w.query, &w.key, &w.value};
+        float *const qkv_c[3] = {q, k, v};
+        const int qkv_ld[3] = {s.dim, int(kvd), int(kvd)};
+        const QMat *gu_w[2] = {&w.gate, &w.up};
+        const QMat *wo = &w.output, *wd = &w.down;
+        float *const gu_c[2] = {g, u};
+        const int gu_ld[2] = {s.ffn_dim, s.ffn_dim};
+        launch_rmsnorm_rows(h, w.attention_norm, xh, xh + size_t(t) * s.dim, t, s.dim,
+                            m.stream);
+        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, qkv_c, qkv_ld, 3, false,
+                          m.stream);
         launch_rope_store(q, k, v, m.rope.as<float2>(), kc, vc, s, t, 0, m.stream);
-        launch_attention_prefill(q, kc, vc, ctx, s, t, 0, m.stream);
-        launch_qgemm_rows(ctx, t, w.output, h, s.dim, true, m.stream);
-        launch_rmsnorm_rows(h, w.ffn_norm, x, t, s.dim, m.stream);
-        launch_qgemm_rows(x, t, w.gate, g, s.ffn_dim, false, m.stream);
-        launch_qgemm_rows(x, t, w.up, u, s.ffn_dim, false, m.stream);
-        launch_silu_mul(g, u, x, size_t(t) * s.ffn_dim, m.stream);
-        launch_qgemm_rows(x, t, w.down, h, s.dim, true, m.stream);
+        launch_attention_prefill(q, kc, vc, ch, ch + size_t(t) * s.dim, s, t, 0, m.stream);
+        launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, &h, &s.dim, 1, true,
+                          m.stream);
+        launch_rmsnorm_rows(h, w.ffn_norm, xh, xh + size_t(t) * s.dim, t, s.dim, m.stream);
+        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, gu_w, gu_c, gu_ld, 2, false,
+                          m.stream);
+        launch_silu_mul(g, u, xh, xh + size_t(t) * s.ffn_dim, size_t(t) * s.ffn_dim,
+                        m.stream);
+        launch_qgemm_rows(xh, xh + size_t(t) * s.ffn_dim, t, &wd, &h, &s.dim, 1, true,
+                          m.stream);
     }
     hip_check(hipMemcpyAsync(m.hidden.get(), h + size_t(t - 1) * s.dim,
                              s.dim * sizeof(float), hipMemcpyDeviceToDevice,

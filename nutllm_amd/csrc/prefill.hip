@@ -31,8 +31,17 @@ __global__ __launch_bounds__(kThreads) void embed_rows_kernel(
 }
 
 // out[t] = h[t] * (1 / sqrt(mean(h[t]^2) + 1e-5)) * w  (src/ops.cpp:111-134)
+// An activation the GEMMs read as two f16 limbs: hi = f16(v), lo =
+// f16(v - hi), so hi + lo carries v to about 2^-22 relative.
+__device__ __forceinline__ void put_limbs(_Float16 *hi, _Float16 *lo, size_t i, float v)
+{
+    const _Float16 a = (_Float16)v;
+    hi[i] = a;
+    lo[i] = (_Float16)(v - (float)a);
+}
+
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
-    const float *h, const float *w, float *out, int dim)
+    const float *h, const float *w, _Float16 *out_hi, _Float16 *out_lo, int dim)
 {
     __shared__ float red[kThreads / kWave];
     const float *x = h + size_t(blockIdx.x) * dim;
@@ -41,20 +50,21 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
         sq = fmaf(x[i], x[i], sq);
     const float total = block_sum(sq, red, kThreads / kWave);
     const float scale = 1.0f / sqrtf(total / float(dim) + 1e-5f);
-    float *o = out + size_t(blockIdx.x) * dim;
+    const size_t row = size_t(blockIdx.x) * dim;
     for (int i = threadIdx.x; i < dim; i += kThreads)
-        o[i] = x[i] * scale * w[i];
+        put_limbs(out_hi, out_lo, row + i, x[i] * scale * w[i]);
 }
 
 // act[t][i] = silu(g[t][i]) * u[t][i]  (src/quant_model.cpp:197-198)
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *g,
                                                             const float *u,
-                                                            float *act, size_t n)
+                                                            _Float16 *act_hi,
+                                                            _Float16 *act_lo, size_t n)
 {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
     if (i < n) {
         const float v = g[i];
-        act[i] = v / (1.0f + expf(-v)) * u[i];
+        put_limbs(act_hi, act_lo, i, v / (1.0f + expf(-v)) * u[i]);
     }
 }
 
@@ -97,74 +107,100 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
 // k % 32 == 0), on v_mfma_f32_16x16x32_f16, whose K = 32 is one quant
 // block:
 //   * W codes q (INT4 -8..7, INT8 -128..127) are exact in f16;
-//   * X is split into two f16 limbs, hi = f16(x) and lo = f16(x - hi), so
-//     hi + lo carries x to about 2^-22 relative (f16 subnormals aside);
+//   * X arrives as two f16 limbs, hi = f16(x) and lo = f16(x - hi), so
+//     hi + lo carries x to about 2^-22 relative (f16 subnormals aside),
+//     written by the kernel that produces X (put_limbs);
 //   * every product of two f16 values is exact in the fp32 accumulator;
 //   * per block, D = A_hi B + A_lo B, then acc += s_n D with the block's
 //     fp16 scale s_n (one column n per lane in the D layout).
-// A workgroup owns 128 tokens x 128 outputs; four waves of 4 x 4 MFMA
-// tiles (64 x 64 each). Per 32-wide k slice the limbs of X and the W codes
-// go to LDS (double-buffered), and the next slice is loaded into registers
-// during the MFMAs. Lane layout (measured): A[i][k] in lane i % 16 + 16 g
+// A workgroup owns FM tokens x 128 outputs; four waves of (FM / 32) x 4
+// MFMA tiles. Per 32-wide k slice the limbs of X and the W
+// codes go to LDS (double-buffered) while the next three slices load into
+// registers. Lane layout (measured): A[i][k] in lane i % 16 + 16 g
 // holding k = 8 g .. 8 g + 7; B[k][n] likewise with n = lane % 16;
 // D[i][n] in lane n + 16 (i / 4), element i % 4.
-constexpr int FM = 128, FN = 128, FK = 32;
+constexpr int FN = 128, FK = 32;
 constexpr int FROW = FK + 8; // f16 per LDS row (16-byte pad)
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-template <int QT, bool ADD>
+// Up to three matrices sharing X and k (Q/K/V, or gate/up) in one launch:
+// column tiles of FN outputs are numbered across the segments in order.
+struct GemmSegs {
+    QMat w[3];
+    float *c[3];
+    int ldc[3];
+    int tiles[3];
+    int count;
+};
+
+template <int QT, bool ADD, int FM>
 __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
-    const float *__restrict__ x, int t_count, QMat w, float *__restrict__ c, int ldc)
+    const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
+    GemmSegs segs)
 {
+    constexpr int MT = FM / 32; // 16-row MFMA tiles per wave (waves 2 x 2)
     __shared__ __attribute__((aligned(16))) _Float16 xh[2][FM][FROW];
     __shared__ __attribute__((aligned(16))) _Float16 xl[2][FM][FROW];
     __shared__ __attribute__((aligned(16))) _Float16 wq[2][FN][FROW];
     __shared__ float wsc[2][FN];
+    int seg = 0, tile = blockIdx.x;
+    while (seg + 1 < segs.count && tile >= segs.tiles[seg])
+        tile -= segs.tiles[seg++]; // workgroup-uniform
+    const QMat w = segs.w[seg];
+    float *__restrict__ c = segs.c[seg];
+    const int ldc = segs.ldc[seg];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * FM, n0 = blockIdx.x * FN;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int t0 = blockIdx.y * FM, n0 = tile * FN;
+    const int wm = (wave >> 1) * (FM / 2), wn = (wave & 1) * 64;
     const int k = w.cols, n_count = w.rows, blocks = k / FK;
-    // loader: row r = tid / 2 of both tiles, 16 consecutive k from 16 h
+    // W loader: row r = tid / 2, 16 consecutive k from 16 h; X loader: the
+    // same for rows r < FM (FM = 64: the upper half of the threads idle)
     const int r = tid >> 1, h = tid & 1;
+    const bool xload = r < FM;
     const int xrow = t0 + r;
-    const float *xp = x + size_t(min(xrow, t_count - 1)) * k + 16 * h;
+    const size_t xoff = size_t(min(xrow, t_count - 1)) * k + 16 * h;
+    const _Float16 *xph = x_hi + xoff, *xpl = x_lo + xoff;
     const int wrow = min(n0 + r, n_count - 1);
     constexpr int RB_DIV = QT == 1 ? 2 : 1;
     const uint8_t *wp = w.data + size_t(wrow) * (k / RB_DIV) + (QT == 1 ? 8 : 16) * h;
     const uint16_t *sp = w.scales + size_t(wrow) * blocks;
-    float4 rx[4];
-    uint4 rw; // INT4 uses .x, .y (16 nibbles); INT8 all (16 bytes)
-    uint16_t rs = 0;
-    auto load = [&](int kb) {
-        const float4 *src = reinterpret_cast<const float4 *>(xp + kb * FK);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            rx[j] = xrow < t_count ? src[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (QT == 1) {
-            const uint2 v = *reinterpret_cast<const uint2 *>(wp + kb * (FK / 2));
-            rw = make_uint4(v.x, v.y, 0u, 0u);
-        } else {
-            rw = *reinterpret_cast<const uint4 *>(wp + kb * FK);
-        }
-        if (h == 0)
-            rs = sp[kb];
+    // One k slice in registers: X limbs, W bytes (INT4 uses .x, .y), scale.
+    struct Slice {
+        half8 xh[2], xl[2];
+        uint4 w;
+        uint16_t s;
     };
-    auto stage = [&](int buf) {
-        half8 hi[2], lo[2];
+    auto load = [&](Slice &sl, int kb) {
+        if (xload) {
+            const half8 *sh = reinterpret_cast<const half8 *>(xph + kb * FK);
+            const half8 *sx = reinterpret_cast<const half8 *>(xpl + kb * FK);
+            const half8 zero = {};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float v[4] = {rx[j].x, rx[j].y, rx[j].z, rx[j].w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const _Float16 a = (_Float16)v[e];
-                hi[j >> 1][4 * (j & 1) + e] = a;
-                lo[j >> 1][4 * (j & 1) + e] = (_Float16)(v[e] - (float)a);
+            for (int j = 0; j < 2; j++) {
+                sl.xh[j] = xrow < t_count ? sh[j] : zero;
+                sl.xl[j] = xrow < t_count ? sx[j] : zero;
             }
         }
+        if (QT == 1) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(wp + kb * (FK / 2));
+            sl.w = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            sl.w = *reinterpret_cast<const uint4 *>(wp + kb * FK);
+        }
+        if (h == 0)
+            sl.s = sp[kb];
+    };
+    auto stage = [&](const Slice &sl, int buf) {
+        if (xload) {
+            *reinterpret_cast<half8 *>(&xh[buf][r][16 * h]) = sl.xh[0];
+            *reinterpret_cast<half8 *>(&xh[buf][r][16 * h + 8]) = sl.xh[1];
+            *reinterpret_cast<half8 *>(&xl[buf][r][16 * h]) = sl.xl[0];
+            *reinterpret_cast<half8 *>(&xl[buf][r][16 * h + 8]) = sl.xl[1];
+        }
         half8 q[2];
-        const uint32_t words[4] = {rw.x, rw.y, rw.z, rw.w};
+        const uint32_t words[4] = {sl.w.x, sl.w.y, sl.w.z, sl.w.w};
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             int code;
@@ -176,33 +212,23 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
             }
             q[e >> 3][e & 7] = (_Float16)code;
         }
-        *reinterpret_cast<half8 *>(&xh[buf][r][16 * h]) = hi[0];
-        *reinterpret_cast<half8 *>(&xh[buf][r][16 * h + 8]) = hi[1];
-        *reinterpret_cast<half8 *>(&xl[buf][r][16 * h]) = lo[0];
-        *reinterpret_cast<half8 *>(&xl[buf][r][16 * h + 8]) = lo[1];
         *reinterpret_cast<half8 *>(&wq[buf][r][16 * h]) = q[0];
         *reinterpret_cast<half8 *>(&wq[buf][r][16 * h + 8]) = q[1];
         if (h == 0)
-            wsc[buf][r] = half_bits_to_float(rs);
+            wsc[buf][r] = half_bits_to_float(sl.s);
     };
-    floatx4 acc[4][4];
+    floatx4 acc[MT][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    load(0);
-    stage(0);
-    __syncthreads();
     const int g = lane >> 4, li = lane & 15;
-    for (int kb = 0; kb < blocks; kb++) {
-        const int buf = kb & 1;
-        if (kb + 1 < blocks)
-            load(kb + 1);
-        half8 ah[4], al[4], b[4];
+    auto compute = [&](int buf) {
+        half8 ah[MT], al[MT], b[4];
         float sc[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < MT; i++) {
             ah[i] = *reinterpret_cast<const half8 *>(&xh[buf][wm + 16 * i + li][8 * g]);
             al[i] = *reinterpret_cast<const half8 *>(&xl[buf][wm + 16 * i + li][8 * g]);
         }
@@ -212,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
             sc[j] = wsc[buf][wn + 16 * j + li];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < MT; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -222,12 +248,34 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
                 for (int v = 0; v < 4; v++)
                     acc[i][j][v] = fmaf(sc[j], d[v], acc[i][j][v]);
             }
+    };
+    // Slices kb .. kb + 2 are in flight in three register sets (slice s in
+    // set s % 3) while slice kb is multiplied from LDS buffer kb % 2.
+    Slice s0, s1, s2;
+    load(s0, 0);
+    if (1 < blocks)
+        load(s1, 1);
+    if (2 < blocks)
+        load(s2, 2);
+    stage(s0, 0);
+    __syncthreads();
+    auto step = [&](int kb, Slice &next, Slice &done) {
+        compute(kb & 1);
         if (kb + 1 < blocks)
-            stage(buf ^ 1);
+            stage(next, (kb + 1) & 1);
+        if (kb + 3 < blocks)
+            load(done, kb + 3);
         __syncthreads();
+    };
+    for (int kb = 0; kb < blocks; kb += 3) {
+        step(kb, s1, s0);
+        if (kb + 1 < blocks)
+            step(kb + 1, s2, s1);
+        if (kb + 2 < blocks)
+            step(kb + 2, s0, s2);
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
@@ -240,8 +288,6 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
                 }
             }
 }
-
-// ------------------------------------------------ causal attention --
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
 // start + t attend to cache positions 0 .. start + t, in 64-key tiles.
@@ -257,8 +303,9 @@ constexpr int AQ = 64, AK = 64;
 // n + 16 k, D[i][n] in lane n + 16 (i / 4), element i % 4.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
-    const float *q, const float *k_cache, const float *v_cache, float *ctx,
-    int t_count, int heads, int kv_heads, int max_seq, int start, float scale)
+    const float *q, const float *k_cache, const float *v_cache, _Float16 *ctx_hi,
+    _Float16 *ctx_lo, int t_count, int heads, int kv_heads, int max_seq, int start,
+    float scale)
 {
     constexpr int KP = HD + 4, VP = HD + 16, PP = AK + 4;
     __shared__ float ks[AK][KP];
@@ -366,25 +413,36 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
         const int t = t0 + 16 * wave + 4 * lg + v;
         if (t < t_count) {
             const float inv = 1.0f / l[v];
-            float *out = ctx + size_t(t) * dim + head * HD;
+            const size_t row = size_t(t) * dim + head * HD;
 #pragma unroll
             for (int dt = 0; dt < HD / 16; dt++)
-                out[16 * dt + li] = o[dt][v] * inv;
+                put_limbs(ctx_hi, ctx_lo, row + 16 * dt + li, o[dt][v] * inv);
         }
     }
 }
 
-template <int QT>
-void launch_qgemm(const float *x, int t_count, const QMat &w, float *c, int ldc,
-                  bool add, hipStream_t stream)
+template <int QT, bool ADD, int FM>
+void launch_qgemm_fm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                     const GemmSegs &segs, hipStream_t stream)
 {
-    const dim3 grid((w.rows + FN - 1) / FN, (t_count + FM - 1) / FM);
+    int tiles = 0;
+    for (int i = 0; i < segs.count; i++)
+        tiles += segs.tiles[i];
+    hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, FM>), dim3(tiles, (t_count + FM - 1) / FM),
+                       dim3(kThreads), 0, stream, x_hi, x_lo, t_count, segs);
+}
+
+// 64-token tiles: with three slices in flight the 128-token tile needs
+// more than 256 registers and runs one wave per SIMD, which measured slower
+// on every prefill shape.
+template <int QT>
+void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                  const GemmSegs &segs, bool add, hipStream_t stream)
+{
     if (add)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true>), grid, dim3(kThreads), 0,
-                           stream, x, t_count, w, c, ldc);
+        launch_qgemm_fm<QT, true, 64>(x_hi, x_lo, t_count, segs, stream);
     else
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false>), grid, dim3(kThreads), 0,
-                           stream, x, t_count, w, c, ldc);
+        launch_qgemm_fm<QT, false, 64>(x_hi, x_lo, t_count, segs, stream);
 }
 
 } // namespace
@@ -407,21 +465,33 @@ void launch_embed_rows(const float *embeddings, const int *tokens, float *h,
     check_launch("prefill embed");
 }
 
-void launch_rmsnorm_rows(const float *h, const float *w, float *out,
-                         int t_count, int dim, hipStream_t stream)
+void launch_rmsnorm_rows(const float *h, const float *w, _Float16 *out_hi,
+                         _Float16 *out_lo, int t_count, int dim, hipStream_t stream)
 {
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(t_count), dim3(kThreads), 0,
-                       stream, h, w, out, dim);
+                       stream, h, w, out_hi, out_lo, dim);
     check_launch("prefill rmsnorm");
 }
 
-void launch_qgemm_rows(const float *x, int t_count, const QMat &w, float *c,
-                       int ldc, bool add, hipStream_t stream)
+void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                       const QMat *const *w, float *const *c, const int *ldc, int count,
+                       bool add, hipStream_t stream)
 {
-    if (w.type == 1)
-        launch_qgemm<1>(x, t_count, w, c, ldc, add, stream);
+    require(count >= 1 && count <= 3, NUT_EINVAL, "prefill gemm: 1 to 3 matrices");
+    GemmSegs segs{};
+    segs.count = count;
+    for (int i = 0; i < count; i++) {
+        require(w[i]->type == w[0]->type && w[i]->cols == w[0]->cols, NUT_EINVAL,
+                "prefill gemm: matrices differ in type or input size");
+        segs.w[i] = *w[i];
+        segs.c[i] = c[i];
+        segs.ldc[i] = ldc[i];
+        segs.tiles[i] = (w[i]->rows + FN - 1) / FN;
+    }
+    if (w[0]->type == 1)
+        launch_qgemm<1>(x_hi, x_lo, t_count, segs, add, stream);
     else
-        launch_qgemm<0>(x, t_count, w, c, ldc, add, stream);
+        launch_qgemm<0>(x_hi, x_lo, t_count, segs, add, stream);
     check_launch("prefill gemm");
 }
 
@@ -437,28 +507,28 @@ void launch_rope_store(float *q, const float *k, const float *v,
 }
 
 void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, float *ctx,
+                              const float *v_cache, _Float16 *ctx_hi, _Float16 *ctx_lo,
                               const DecodeShape &s, int t_count, int start,
                               hipStream_t stream)
 {
     const dim3 grid((t_count + AQ - 1) / AQ, s.heads);
     if (s.head_dim == 128)
         hipLaunchKernelGGL(attention_prefill_mfma<128>, grid, dim3(kThreads), 0,
-                           stream, q, k_cache, v_cache, ctx, t_count, s.heads,
+                           stream, q, k_cache, v_cache, ctx_hi, ctx_lo, t_count, s.heads,
                            s.kv_heads, s.max_seq, start, s.attn_scale);
     else
         hipLaunchKernelGGL(attention_prefill_mfma<64>, grid, dim3(kThreads), 0,
-                           stream, q, k_cache, v_cache, ctx, t_count, s.heads,
+                           stream, q, k_cache, v_cache, ctx_hi, ctx_lo, t_count, s.heads,
                            s.kv_heads, s.max_seq, start, s.attn_scale);
     check_launch("prefill attention");
 }
 
-void launch_silu_mul(const float *g, const float *u, float *act, size_t n,
-                     hipStream_t stream)
+void launch_silu_mul(const float *g, const float *u, _Float16 *act_hi,
+                     _Float16 *act_lo, size_t n, hipStream_t stream)
 {
     const int blocks = int((n + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(kThreads), 0, stream,
-                       g, u, act, n);
+                       g, u, act_hi, act_lo, n);
     check_launch("prefill silu");
 }
 

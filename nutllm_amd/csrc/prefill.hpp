@@ -14,12 +14,16 @@ bool prefill_gemm_supported(const DecodeShape &s, const LayerView &w);
 
 void launch_embed_rows(const float *embeddings, const int *tokens, float *h,
                        int t_count, int dim, hipStream_t stream);
-void launch_rmsnorm_rows(const float *h, const float *w, float *out,
-                         int t_count, int dim, hipStream_t stream);
-// c[t][n] (= or +=) sum_k x[t][k] w[n][k], t < t_count; x rows are w.cols
-// floats, c rows ldc floats.
-void launch_qgemm_rows(const float *x, int t_count, const QMat &w, float *c,
-                       int ldc, bool add, hipStream_t stream);
+// GEMM inputs are written as two f16 limbs per value: hi = f16(v) and
+// lo = f16(v - hi), [t][k] each.
+void launch_rmsnorm_rows(const float *h, const float *w, _Float16 *out_hi,
+                         _Float16 *out_lo, int t_count, int dim, hipStream_t stream);
+// c_i[t][n] (= or +=) sum_k x[t][k] w_i[n][k] for `count` (1 to 3)
+// matrices of one type and input size, t < t_count, in one launch; x as
+// limbs of w.cols values per row, c_i rows ldc_i floats.
+void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                       const QMat *const *w, float *const *c, const int *ldc, int count,
+                       bool add, hipStream_t stream);
 // RoPE of q rows and k rows at positions start + t; k and v rows into the
 // layer's cache.
 void launch_rope_store(float *q, const float *k, const float *v,
@@ -29,10 +33,10 @@ void launch_rope_store(float *q, const float *k, const float *v,
 // Causal attention of the t_count queries over cache positions
 // 0 .. start + t.
 void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, float *ctx,
+                              const float *v_cache, _Float16 *ctx_hi, _Float16 *ctx_lo,
                               const DecodeShape &s, int t_count, int start,
                               hipStream_t stream);
-void launch_silu_mul(const float *g, const float *u, float *act, size_t n,
-                     hipStream_t stream);
+void launch_silu_mul(const float *g, const float *u, _Float16 *act_hi,
+                     _Float16 *act_lo, size_t n, hipStream_t stream);
 
 } // namespace nut
