@@ -170,7 +170,9 @@ __device__ __forceinline__ float max_lanes_0_2(float v)
 
 // Tagged words of the split results: (tag << 32) | value bits, stored and
 // loaded at agent scope, so every XCD sees them whatever its L2 holds. A
-// word read with the wrong tag is one whose store has not arrived yet.
+// word read with the wrong tag is one whose store has not arrived yet; the
+// merge re-reads such words at most kMergeSpin times, then takes NaN (which
+// shows in the context).
 constexpr int kMergeSpin = 1 << 20;
 
 __device__ __forceinline__ void publish(uint64_t *p, float v, uint32_t tag)
@@ -182,19 +184,6 @@ __device__ __forceinline__ void publish(uint64_t *p, float v, uint32_t tag)
 __device__ __forceinline__ uint64_t take_word(const uint64_t *p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The value of word w at p once it carries tag (bounded re-polling; NaN if
-// it never does, which shows in the context).
-__device__ __forceinline__ float tagged_value(uint64_t w, const uint64_t *p, uint32_t tag)
-{
-    for (int spin = 0; uint32_t(w >> 32) != tag; spin++) {
-        if (spin >= kMergeSpin)
-            return __builtin_nanf("");
-        __builtin_amdgcn_s_sleep(1);
-        w = take_word(p);
-    }
-    return __uint_as_float(uint32_t(w));
 }
 
 // Attention of query heads [G row, G row + G), row = blockIdx.x, over
@@ -254,7 +243,6 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
     __shared__ float wmax[2][kWaves][G];
     __shared__ float red[kWaves][G][HD];
     __shared__ float lred[kWaves][G];
-    __shared__ float mls[kAttnMaxSplits][G][2];
     __shared__ float fw[kAttnMaxSplits][G];
     __shared__ int last;
 
@@ -419,52 +407,90 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(
     __syncthreads();
     if (!last)
         return;
-    // merge: every word is requested at once; the weights
-    // exp(m_s - M) / L of every (split, head) go through LDS meanwhile
+    // merge: every word is requested at once. Lane sp of a 32-lane half
+    // wave takes (m, l) of split sp of one head, so the weights
+    // exp(m_s - M) / L come from DPP and one cross-row swap, into LDS; then
+    // the context words are re-read together until all carry the tag.
     const uint64_t *ml = ml_part + size_t(row) * gridDim.y * G * 2;
     const uint64_t *op = o_part + size_t(row) * gridDim.y * G * HD;
     uint64_t a[OUT][kAttnMaxSplits];
 #pragma unroll
     for (int u = 0; u < OUT; u++) {
-        const int t = threadIdx.x + u * kThreads;
+        const int e = threadIdx.x + u * kThreads;
 #pragma unroll
         for (int j = 0; j < kAttnMaxSplits; j++)
-            a[u][j] = t < G * HD && j < splits ? take_word(op + size_t(j) * G * HD + t) : 0;
+            a[u][j] = e < G * HD && j < splits ? take_word(op + size_t(j) * G * HD + e)
+                                               : uint64_t(tag) << 32;
     }
-    if (threadIdx.x < splits * G) {
-        const int sp = threadIdx.x / G, g = threadIdx.x % G;
-        const uint64_t *p = ml + threadIdx.x * 2;
-        const uint64_t w0 = take_word(p), w1 = take_word(p + 1);
-        mls[sp][g][0] = tagged_value(w0, p, tag);
-        mls[sp][g][1] = tagged_value(w1, p + 1, tag);
-    }
-    __syncthreads();
-    if (threadIdx.x < kAttnMaxSplits * G) {
-        const int sp = threadIdx.x / G, g = threadIdx.x % G;
-        float weight = 0.0f;
+    static_assert(kAttnMaxSplits == 32 && 32 * G <= kThreads, "one half wave per head");
+    if (threadIdx.x < 32 * G) {
+        const int g = threadIdx.x / 32, sp = threadIdx.x % 32;
+        const uint64_t *p = ml + (size_t(sp) * G + g) * 2;
+        uint64_t w0 = uint64_t(tag) << 32, w1 = w0;
         if (sp < splits) {
-            float mx = -INFINITY;
-            for (int j = 0; j < splits; j++)
-                mx = fmaxf(mx, mls[j][g][0]);
-            float total = 0.0f;
-            for (int j = 0; j < splits; j++)
-                total = fmaf(mls[j][g][1], expf(mls[j][g][0] - mx), total);
-            weight = expf(mls[sp][g][0] - mx) / total;
+            w0 = take_word(p);
+            w1 = take_word(p + 1);
         }
-        fw[sp][g] = weight;
+        for (int spin = 0; uint32_t(w0 >> 32) != tag || uint32_t(w1 >> 32) != tag; spin++) {
+            if (spin >= kMergeSpin) {
+                w0 = w1 = (uint64_t(tag) << 32) | __float_as_uint(__builtin_nanf(""));
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            if (uint32_t(w0 >> 32) != tag)
+                w0 = take_word(p);
+            if (uint32_t(w1 >> 32) != tag)
+                w1 = take_word(p + 1);
+        }
+        const float mv = sp < splits ? __uint_as_float(uint32_t(w0)) : -INFINITY;
+        const float lv = sp < splits ? __uint_as_float(uint32_t(w1)) : 0.0f;
+        float mx = row16_max(mv);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        const float ev = sp < splits ? expf(mv - mx) : 0.0f;
+        float total = row16_sum(ev * lv);
+        total += __shfl_xor(total, 16);
+        fw[sp][g] = ev / total;
+    }
+    for (int spin = 0;; spin++) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < OUT; u++)
+#pragma unroll
+            for (int j = 0; j < kAttnMaxSplits; j++)
+                stale |= uint32_t(a[u][j] >> 32) != tag;
+        if (!stale)
+            break;
+        if (spin >= kMergeSpin) {
+#pragma unroll
+            for (int u = 0; u < OUT; u++)
+#pragma unroll
+                for (int j = 0; j < kAttnMaxSplits; j++)
+                    if (uint32_t(a[u][j] >> 32) != tag)
+                        a[u][j] = (uint64_t(tag) << 32) | __float_as_uint(__builtin_nanf(""));
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < OUT; u++) {
+            const int e = threadIdx.x + u * kThreads;
+#pragma unroll
+            for (int j = 0; j < kAttnMaxSplits; j++)
+                if (uint32_t(a[u][j] >> 32) != tag)
+                    a[u][j] = take_word(op + size_t(j) * G * HD + e);
+        }
     }
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < OUT; u++) {
-        const int t = threadIdx.x + u * kThreads;
-        if (t < G * HD) {
-            const int g = t / HD;
+        const int e = threadIdx.x + u * kThreads;
+        if (e < G * HD) {
+            const int g = e / HD;
             float o = 0.0f;
 #pragma unroll
             for (int j = 0; j < kAttnMaxSplits; j++)
                 if (j < splits)
-                    o = fmaf(tagged_value(a[u][j], op + size_t(j) * G * HD + t, tag), fw[j][g], o);
-            context[size_t(row * G) * HD + t] = o;
+                    o = fmaf(__uint_as_float(uint32_t(a[u][j])), fw[j][g], o);
+            context[size_t(row * G) * HD + e] = o;
         }
     }
 }
@@ -475,10 +501,14 @@ int blocks_for_rows(int rows, int per_wave)
     return (waves + kWaves - 1) / kWaves;
 }
 
-// Query heads per attention workgroup: two of head_dim 64, one of 128.
+// Query heads per attention workgroup (they share the K/V rows it loads):
+// up to four of head_dim 64, one of 128.
 int attention_group(const DecodeShape &s)
 {
-    return s.head_dim == 64 && (s.heads / s.kv_heads) % 2 == 0 ? 2 : 1;
+    const int group = s.heads / s.kv_heads;
+    if (s.head_dim != 64)
+        return 1;
+    return group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
 }
 
 // Splits of the attention grid: enough workgroups for the chip's 256 CUs,
@@ -509,10 +539,18 @@ void launch_attention_g(const DecodeShape &s, const float *k_layer, const float 
                         const int *length, const StepBuffers &b, int tokens,
                         const StepState *state, hipStream_t stream)
 {
-    if (attention_group(s) == 2)
-        launch_attention<HD, 2>(s, k_layer, v_layer, length, b, tokens, state, stream);
-    else
-        launch_attention<HD, 1>(s, k_layer, v_layer, length, b, tokens, state, stream);
+    const int g = attention_group(s);
+    if constexpr (HD == 64) {
+        if (g == 4) {
+            launch_attention<HD, 4>(s, k_layer, v_layer, length, b, tokens, state, stream);
+            return;
+        }
+        if (g == 2) {
+            launch_attention<HD, 2>(s, k_layer, v_layer, length, b, tokens, state, stream);
+            return;
+        }
+    }
+    launch_attention<HD, 1>(s, k_layer, v_layer, length, b, tokens, state, stream);
 }
 
 template <int QT, int HD>
