@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
 constexpr int AQ = 64, AK = 64;
 
 // On v_mfma_f32_16x16x4f32 (fp32 operands, as the reference's
-// arithmetic): one workgroup per (64-query tile, head);
+// arithmetic): one workgroup per (head, 64-query tile);
 // wave w owns queries 16 w .. 16 w + 15. Per 64-key tile (K and V in LDS):
 // S = Q K^T as 4 x (HD / 4) MFMAs with Q in registers, the online softmax
 // on S in registers (a query row lives in one 16-lane DPP row), P through
@@ -313,8 +313,10 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
     __shared__ float ps[4][16][PP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int head = blockIdx.y, g = head / (heads / kv_heads);
-    const int t0 = blockIdx.x * AQ;
+    // heads vary fastest and the longest query tiles (the most key tiles
+    // under the causal mask) are dispatched first
+    const int head = blockIdx.x, g = head / (heads / kv_heads);
+    const int t0 = (gridDim.y - 1 - blockIdx.y) * AQ;
     const int dim = heads * HD;
     // Q fragments of this wave's rows: A[i = li][k = 4 s + lg]
     float qa[HD / 4];
@@ -511,7 +513,7 @@ void launch_attention_prefill(const float *q, const float *k_cache,
                               const DecodeShape &s, int t_count, int start,
                               hipStream_t stream)
 {
-    const dim3 grid((t_count + AQ - 1) / AQ, s.heads);
+    const dim3 grid(s.heads, (t_count + AQ - 1) / AQ);
     if (s.head_dim == 128)
         hipLaunchKernelGGL(attention_prefill_mfma<128>, grid, dim3(kThreads), 0,
                            stream, q, k_cache, v_cache, ctx_hi, ctx_lo, t_count, s.heads,
