@@ -119,10 +119,21 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
 // registers. Lane layout (measured): A[i][k] in lane i % 16 + 16 g
 // holding k = 8 g .. 8 g + 7; B[k][n] likewise with n = lane % 16;
 // D[i][n] in lane n + 16 (i / 4), element i % 4.
-constexpr int FN = 128, FK = 32;
-constexpr int FROW = FK + 8; // f16 per LDS row (16-byte pad)
+constexpr int FM_ROWS = 64, FN = 128, FK = 32;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Two quantisation codes as two f16 (exact): an offset-binary code u sits
+// in the low byte of an f16 whose high byte is 0x64, which is the value
+// 1024 + u; subtracting 1024 + bias gives the code. `pair` holds such a
+// word for two codes.
+__device__ __forceinline__ uint32_t codes_from_pair(uint32_t pair, float bias)
+{
+    const half2v v = __builtin_bit_cast(half2v, pair) -
+                     half2v{(_Float16)(1024.0f + bias), (_Float16)(1024.0f + bias)};
+    return __builtin_bit_cast(uint32_t, v);
+}
 
 // Up to three matrices sharing X and k (Q/K/V, or gate/up) in one launch:
 // column tiles of FN outputs are numbered across the segments in order.
@@ -134,113 +145,245 @@ struct GemmSegs {
     int count;
 };
 
-template <int QT, bool ADD, int FM>
+// ------------------------------------------------------ quantised GEMM --
+
+// C[t][n] (+)= sum_k x[t][k] q[n][k] s[n][k / 32] for a 64-token x 128-row
+// tile per workgroup, one 32-wide k slice (one quant block) per step.
+// Operands reach LDS by DMA (global_load_lds_dwordx4) into a ring of
+// kSlots slices, so three slices load while one is multiplied and no
+// register holds them in flight. Per slice: x_hi and x_lo (64 rows x 64 B
+// each; the four 16-byte granules of a row XOR-swizzled by (row >> 1) & 3
+// so that the A-fragment reads of 8 consecutive rows hit distinct banks),
+// the weight bytes (128 rows x 32 B for INT8, x 16 B for INT4; INT8 row
+// halves swizzled by (row >> 2) & 1) and the dword of each row's scales
+// that holds the slice's fp16 scale.
+// Wave w multiplies all 64 tokens by rows [32 w, 32 w + 32): 4 x 2 tiles
+// of v_mfma_f32_16x16x32_f16, A = x limbs (hi and lo, two MFMAs per tile),
+// B = the codes, dequantised exactly into f16 from the wave's own rows;
+// then acc += s_n * D per tile. Lane layouts (checked on the device):
+// A[i][k]: lane i % 16 + 16 g holds k = 8 g .. 8 g + 7; B[k][n]: lane
+// n % 16 + 16 g the same k; D[i][n]: lane n + 16 (i / 4), element i % 4.
+constexpr int kSlots = 4;
+constexpr int kDmaPerWave = 4; // DMA instructions per wave per slice
+
+template <int QT> struct GemmSlot {
+    uint4 xh[FM_ROWS * 4];
+    uint4 xl[FM_ROWS * 4];
+    uint4 w[QT == 1 ? FN : 2 * FN];
+    uint32_t sc[FN];
+};
+
+// s_waitcnt with only vmcnt = n (expcnt and lgkmcnt left at their maxima).
+constexpr int vm_wait(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+__device__ __forceinline__ void dma16(const void *src, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void *)src,
+        (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ void dma4(const void *src, void *lds)
+{
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void *)src,
+        (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
+}
+
+// LDS address (byte offset) of a generic pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return uint32_t(reinterpret_cast<uintptr_t>(
+        (const __attribute__((address_space(3))) char *)(p)));
+}
+
+// Eight codes (k = 8 g .. 8 g + 7 of one row) as f16: INT8 from 8 bytes,
+// INT4 from 4 bytes (even k in the low nibble).
+template <int QT>
+__device__ __forceinline__ half8 codes8(uint2 raw)
+{
+    uint32_t out[4];
+    if (QT == 1) {
+        const uint32_t t = raw.x ^ 0x88888888u, s4 = t >> 4;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t sel = 0x0c000c00u | uint32_t(4 + b) << 16 | uint32_t(b);
+            out[b] = codes_from_pair((__builtin_amdgcn_perm(s4, t, sel) & 0x000f000fu) |
+                                         0x64006400u,
+                                     8.0f);
+        }
+    } else {
+        const uint32_t words[2] = {raw.x, raw.y};
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t t = words[j] ^ 0x80808080u;
+            out[2 * j] = codes_from_pair(__builtin_amdgcn_perm(0x64646464u, t, 0x04010400u), 128.0f);
+            out[2 * j + 1] =
+                codes_from_pair(__builtin_amdgcn_perm(0x64646464u, t, 0x04030402u), 128.0f);
+        }
+    }
+    return __builtin_bit_cast(half8, make_uint4(out[0], out[1], out[2], out[3]));
+}
+
+template <int QT, bool ADD>
 __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
     GemmSegs segs)
 {
-    constexpr int MT = FM / 32; // 16-row MFMA tiles per wave (waves 2 x 2)
-    __shared__ __attribute__((aligned(16))) _Float16 xh[2][FM][FROW];
-    __shared__ __attribute__((aligned(16))) _Float16 xl[2][FM][FROW];
-    __shared__ __attribute__((aligned(16))) _Float16 wq[2][FN][FROW];
-    __shared__ float wsc[2][FN];
+    __shared__ GemmSlot<QT> slot0, slot1, slot2, slot3;
+    __shared__ uint4 junk[kWave];
     int seg = 0, tile = blockIdx.x;
     while (seg + 1 < segs.count && tile >= segs.tiles[seg])
         tile -= segs.tiles[seg++]; // workgroup-uniform
     const QMat w = segs.w[seg];
     float *__restrict__ c = segs.c[seg];
     const int ldc = segs.ldc[seg];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * FM, n0 = tile * FN;
-    const int wm = (wave >> 1) * (FM / 2), wn = (wave & 1) * 64;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
     const int k = w.cols, n_count = w.rows, blocks = k / FK;
-    // W loader: row r = tid / 2, 16 consecutive k from 16 h; X loader: the
-    // same for rows r < FM (FM = 64: the upper half of the threads idle)
-    const int r = tid >> 1, h = tid & 1;
-    const bool xload = r < FM;
-    const int xrow = t0 + r;
-    const size_t xoff = size_t(min(xrow, t_count - 1)) * k + 16 * h;
-    const _Float16 *xph = x_hi + xoff, *xpl = x_lo + xoff;
-    const int wrow = min(n0 + r, n_count - 1);
-    constexpr int RB_DIV = QT == 1 ? 2 : 1;
-    const uint8_t *wp = w.data + size_t(wrow) * (k / RB_DIV) + (QT == 1 ? 8 : 16) * h;
-    const uint16_t *sp = w.scales + size_t(wrow) * blocks;
-    // One k slice in registers: X limbs, W bytes (INT4 uses .x, .y), scale.
-    struct Slice {
-        half8 xh[2], xl[2];
-        uint4 w;
-        uint16_t s;
+    const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
+    const int scale_words = blocks / 2; // dwords of scales per row
+
+    // This lane's part of the wave's four DMA instructions per slice (all
+    // waves issue four, so one vmcnt value covers every wave): 0 = x_hi rows
+    // 16 wave + lane / 4, 1 = x_lo the same, 2 = weight rows (INT8: 32 per
+    // wave; INT4: 64 per wave for waves 0-1, the scale dwords of rows
+    // 64 (wave - 2) + lane for waves 2-3), 3 = INT8 scale dwords (waves 0-1)
+    // or a filler load into `junk`. Source pointers are at slice 0; a slice
+    // advances them by the slice's byte step.
+    const int xrow = 16 * wave + (lane >> 2);
+    const int xg = (lane & 3) ^ ((xrow >> 1) & 3);
+    const size_t xoff = size_t(min(t0 + xrow, t_count - 1)) * k + 8 * xg;
+    const char *src_xh = reinterpret_cast<const char *>(x_hi + xoff);
+    const char *src_xl = reinterpret_cast<const char *>(x_lo + xoff);
+    const char *src_w, *src_s;
+    int w_lds, s_lds;
+    bool w_is_scale, s_is_filler;
+    if (QT == 1) {
+        const int wrow = kWave * wave + lane; // waves 0-1
+        const int srow = kWave * (wave - 2) + lane; // waves 2-3
+        w_is_scale = wave >= 2;
+        const int r = w_is_scale ? srow : wrow;
+        src_w = w_is_scale ? reinterpret_cast<const char *>(w.scales) +
+                                 size_t(min(n0 + r, n_count - 1)) * scale_words * 4
+                           : reinterpret_cast<const char *>(w.data) +
+                                 size_t(min(n0 + r, n_count - 1)) * row_bytes;
+        w_lds = w_is_scale ? kWave * (wave - 2) : kWave * wave;
+        s_is_filler = true;
+        src_s = reinterpret_cast<const char *>(x_hi);
+        s_lds = 0;
+    } else {
+        const int wrow = 32 * wave + (lane >> 1);
+        const int gran = (lane & 1) ^ ((wrow >> 2) & 1);
+        w_is_scale = false;
+        src_w = reinterpret_cast<const char *>(w.data) +
+                size_t(min(n0 + wrow, n_count - 1)) * row_bytes + 16 * gran;
+        w_lds = kWave * wave;
+        s_is_filler = wave >= 2;
+        const int srow = kWave * wave + lane;
+        src_s = s_is_filler ? reinterpret_cast<const char *>(x_hi)
+                            : reinterpret_cast<const char *>(w.scales) +
+                                  size_t(min(n0 + srow, n_count - 1)) * scale_words * 4;
+        s_lds = kWave * wave;
+    }
+    auto issue = [&](GemmSlot<QT> &sl, int kb) {
+        kb = min(kb, blocks - 1); // past the end: reload the last slice
+        dma16(src_xh + size_t(kb) * (FK * 2), &sl.xh[kWave * wave]);
+        dma16(src_xl + size_t(kb) * (FK * 2), &sl.xl[kWave * wave]);
+        if (w_is_scale) // workgroup-uniform per wave
+            dma4(src_w + 4 * (kb >> 1), &sl.sc[w_lds]);
+        else
+            dma16(src_w + size_t(kb) * (QT == 1 ? 16 : 32), &sl.w[w_lds]);
+        if (s_is_filler)
+            dma16(src_s, &junk[0]);
+        else
+            dma4(src_s + 4 * (kb >> 1), &sl.sc[s_lds]);
     };
-    auto load = [&](Slice &sl, int kb) {
-        if (xload) {
-            const half8 *sh = reinterpret_cast<const half8 *>(xph + kb * FK);
-            const half8 *sx = reinterpret_cast<const half8 *>(xpl + kb * FK);
-            const half8 zero = {};
+
+    floatx4 acc[4][2];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                sl.xh[j] = xrow < t_count ? sh[j] : zero;
-                sl.xl[j] = xrow < t_count ? sx[j] : zero;
-            }
-        }
-        if (QT == 1) {
-            const uint2 v = *reinterpret_cast<const uint2 *>(wp + kb * (FK / 2));
-            sl.w = make_uint4(v.x, v.y, 0u, 0u);
-        } else {
-            sl.w = *reinterpret_cast<const uint4 *>(wp + kb * FK);
-        }
-        if (h == 0)
-            sl.s = sp[kb];
-    };
-    auto stage = [&](const Slice &sl, int buf) {
-        if (xload) {
-            *reinterpret_cast<half8 *>(&xh[buf][r][16 * h]) = sl.xh[0];
-            *reinterpret_cast<half8 *>(&xh[buf][r][16 * h + 8]) = sl.xh[1];
-            *reinterpret_cast<half8 *>(&xl[buf][r][16 * h]) = sl.xl[0];
-            *reinterpret_cast<half8 *>(&xl[buf][r][16 * h + 8]) = sl.xl[1];
-        }
-        half8 q[2];
-        const uint32_t words[4] = {sl.w.x, sl.w.y, sl.w.z, sl.w.w};
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            int code;
-            if (QT == 1) {
-                const uint32_t nib = (words[e >> 3] >> (4 * (e & 7))) & 0xfu;
-                code = int(nib) - (nib >= 8 ? 16 : 0);
-            } else {
-                code = int(int8_t((words[e >> 2] >> (8 * (e & 3))) & 0xffu));
-            }
-            q[e >> 3][e & 7] = (_Float16)code;
-        }
-        *reinterpret_cast<half8 *>(&wq[buf][r][16 * h]) = q[0];
-        *reinterpret_cast<half8 *>(&wq[buf][r][16 * h + 8]) = q[1];
-        if (h == 0)
-            wsc[buf][r] = half_bits_to_float(sl.s);
-    };
-    floatx4 acc[MT][4];
-#pragma unroll
-    for (int i = 0; i < MT; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const int g = lane >> 4, li = lane & 15;
-    auto compute = [&](int buf) {
-        half8 ah[MT], al[MT], b[4];
-        float sc[4];
+    // A fragments of rows 16 i + li (the swizzle (row >> 1) & 3 does not
+    // depend on i), B bytes and scale dwords of rows n = 32 wave + 16 j + li
+    // (the INT8 swizzle (n >> 2) & 1 does not depend on j): three base
+    // addresses per slot, constant offsets.
+    const uint32_t a_off = 16 * (4 * li + (g ^ ((li >> 1) & 3)));
+    const int n_lane = 32 * wave + li;
+    const uint32_t b_off = QT == 1 ? 16 * n_lane + 4 * g
+                                   : 32 * n_lane + 16 * ((g >> 1) ^ ((li >> 2) & 1)) + 8 * (g & 1);
+    // The slot's operands, read in one asm block that ends with lgkmcnt(0):
+    // the reads are not matched against the DMA still in flight into the
+    // other ring slots (the compiler would wait for all of it), and every
+    // result depends on the wait. The caller's vmcnt wait and barrier have
+    // landed this slot.
+    auto compute = [&](const GemmSlot<QT> &sl, int kb) {
+        uint4 xa[4], xb[4];
+        uint2 raw[2];
+        uint32_t sw[2];
+        const uint32_t a_at = lds_addr(sl.xh) + a_off;
+        const uint32_t b_at = lds_addr(sl.w) + b_off;
+        const uint32_t s_at = lds_addr(sl.sc) + 4 * n_lane;
+        static_assert(sizeof(sl.xh) == 4096, "x_lo follows x_hi at 4 KB");
+        if (QT == 1) {
+            asm volatile("ds_read_b128 %0, %12\n"
+                         "ds_read_b128 %1, %12 offset:1024\n"
+                         "ds_read_b128 %2, %12 offset:2048\n"
+                         "ds_read_b128 %3, %12 offset:3072\n"
+                         "ds_read_b128 %4, %12 offset:4096\n"
+                         "ds_read_b128 %5, %12 offset:5120\n"
+                         "ds_read_b128 %6, %12 offset:6144\n"
+                         "ds_read_b128 %7, %12 offset:7168\n"
+                         "ds_read_b32 %8, %13\n"
+                         "ds_read_b32 %9, %13 offset:256\n"
+                         "ds_read_b32 %10, %14\n"
+                         "ds_read_b32 %11, %14 offset:64\n"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]),
+                           "=&v"(xb[0]), "=&v"(xb[1]), "=&v"(xb[2]), "=&v"(xb[3]),
+                           "=&v"(raw[0].x), "=&v"(raw[1].x), "=&v"(sw[0]), "=&v"(sw[1])
+                         : "v"(a_at), "v"(b_at), "v"(s_at)
+                         : "memory");
+            raw[0].y = raw[1].y = 0;
+        } else {
+            asm volatile("ds_read_b128 %0, %12\n"
+                         "ds_read_b128 %1, %12 offset:1024\n"
+                         "ds_read_b128 %2, %12 offset:2048\n"
+                         "ds_read_b128 %3, %12 offset:3072\n"
+                         "ds_read_b128 %4, %12 offset:4096\n"
+                         "ds_read_b128 %5, %12 offset:5120\n"
+                         "ds_read_b128 %6, %12 offset:6144\n"
+                         "ds_read_b128 %7, %12 offset:7168\n"
+                         "ds_read_b64 %8, %13\n"
+                         "ds_read_b64 %9, %13 offset:512\n"
+                         "ds_read_b32 %10, %14\n"
+                         "ds_read_b32 %11, %14 offset:64\n"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]),
+                           "=&v"(xb[0]), "=&v"(xb[1]), "=&v"(xb[2]), "=&v"(xb[3]),
+                           "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(sw[0]), "=&v"(sw[1])
+                         : "v"(a_at), "v"(b_at), "v"(s_at)
+                         : "memory");
+        }
+        half8 ah[4], al[4], b[2];
+        float sc[2];
 #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            ah[i] = *reinterpret_cast<const half8 *>(&xh[buf][wm + 16 * i + li][8 * g]);
-            al[i] = *reinterpret_cast<const half8 *>(&xl[buf][wm + 16 * i + li][8 * g]);
+        for (int i = 0; i < 4; i++) {
+            ah[i] = __builtin_bit_cast(half8, xa[i]);
+            al[i] = __builtin_bit_cast(half8, xb[i]);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            b[j] = *reinterpret_cast<const half8 *>(&wq[buf][wn + 16 * j + li][8 * g]);
-            sc[j] = wsc[buf][wn + 16 * j + li];
+        for (int j = 0; j < 2; j++) {
+            b[j] = codes8<QT>(raw[j]);
+            sc[j] = half_bits_to_float(uint16_t(sw[j] >> (16 * (kb & 1))));
         }
 #pragma unroll
-        for (int i = 0; i < MT; i++)
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < 2; j++) {
                 floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     ah[i], b[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], d, 0, 0, 0);
@@ -249,44 +392,58 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
                     acc[i][j][v] = fmaf(sc[j], d[v], acc[i][j][v]);
             }
     };
-    // Slices kb .. kb + 2 are in flight in three register sets (slice s in
-    // set s % 3) while slice kb is multiplied from LDS buffer kb % 2.
-    Slice s0, s1, s2;
-    load(s0, 0);
-    if (1 < blocks)
-        load(s1, 1);
-    if (2 < blocks)
-        load(s2, 2);
-    stage(s0, 0);
-    __syncthreads();
-    auto step = [&](int kb, Slice &next, Slice &done) {
-        compute(kb & 1);
-        if (kb + 1 < blocks)
-            stage(next, (kb + 1) & 1);
-        if (kb + 3 < blocks)
-            load(done, kb + 3);
-        __syncthreads();
+    // Slices kb + 1, kb + 2 stay in flight while slice kb is waited for;
+    // slice kb + 3 goes into the slot slice kb - 1 left.
+    // (a plain s_barrier: a workgroup fence would drain every DMA in flight;
+    // each wave's vmcnt wait has already landed its own part of slice kb)
+    auto step = [&](GemmSlot<QT> &cur, GemmSlot<QT> &next3, int kb) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(2 * kDmaPerWave));
+        __builtin_amdgcn_s_barrier();
+        issue(next3, kb + 3);
+        compute(cur, kb);
     };
-    for (int kb = 0; kb < blocks; kb += 3) {
-        step(kb, s1, s0);
+    issue(slot0, 0);
+    issue(slot1, 1);
+    issue(slot2, 2);
+    for (int kb = 0; kb < blocks; kb += kSlots) {
+        step(slot0, slot3, kb);
         if (kb + 1 < blocks)
-            step(kb + 1, s2, s1);
+            step(slot1, slot0, kb + 1);
         if (kb + 2 < blocks)
-            step(kb + 2, s0, s2);
+            step(slot2, slot1, kb + 2);
+        if (kb + 3 < blocks)
+            step(slot3, slot2, kb + 3);
     }
+    __builtin_amdgcn_s_waitcnt(vm_wait(0)); // no DMA outlives the workgroup
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int t = t0 + wm + 16 * i + 4 * g + v;
-                const int n = n0 + wn + 16 * j + li;
+                const int t = t0 + 16 * i + 4 * g + v;
+                const int n = n0 + 32 * wave + 16 * j + li;
                 if (t < t_count && n < n_count) {
                     float *p = c + size_t(t) * ldc + n;
                     *p = ADD ? *p + acc[i][j][v] : acc[i][j][v];
                 }
             }
+}
+
+template <int QT>
+void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                  const GemmSegs &segs, bool add, hipStream_t stream)
+{
+    int tiles = 0;
+    for (int i = 0; i < segs.count; i++)
+        tiles += segs.tiles[i];
+    const dim3 grid(tiles, (t_count + FM_ROWS - 1) / FM_ROWS);
+    if (add)
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true>), grid, dim3(kThreads), 0, stream,
+                           x_hi, x_lo, t_count, segs);
+    else
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false>), grid, dim3(kThreads), 0, stream,
+                           x_hi, x_lo, t_count, segs);
 }
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
@@ -423,38 +580,16 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
     }
 }
 
-template <int QT, bool ADD, int FM>
-void launch_qgemm_fm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
-                     const GemmSegs &segs, hipStream_t stream)
-{
-    int tiles = 0;
-    for (int i = 0; i < segs.count; i++)
-        tiles += segs.tiles[i];
-    hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, FM>), dim3(tiles, (t_count + FM - 1) / FM),
-                       dim3(kThreads), 0, stream, x_hi, x_lo, t_count, segs);
-}
-
-// 64-token tiles: with three slices in flight the 128-token tile needs
-// more than 256 registers and runs one wave per SIMD, which measured slower
-// on every prefill shape.
-template <int QT>
-void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
-                  const GemmSegs &segs, bool add, hipStream_t stream)
-{
-    if (add)
-        launch_qgemm_fm<QT, true, 64>(x_hi, x_lo, t_count, segs, stream);
-    else
-        launch_qgemm_fm<QT, false, 64>(x_hi, x_lo, t_count, segs, stream);
-}
-
 } // namespace
 
 bool prefill_gemm_supported(const DecodeShape &s, const LayerView &w)
 {
     const QMat *mats[7] = {&w.query, &w.key, &w.value, &w.output,
                            &w.gate, &w.up, &w.down};
+    // whole blocks per row, and an even block count (a row's scales are
+    // DMA'd as dwords)
     for (const QMat *m : mats)
-        if (!fast_layout(*m))
+        if (!fast_layout(*m) || m->cols % 64 != 0)
             return false;
     return s.head_dim == 64 || s.head_dim == 128;
 }
