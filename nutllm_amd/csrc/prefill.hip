@@ -148,53 +148,71 @@ struct GemmSegs {
 // ------------------------------------------------------ quantised GEMM --
 
 // C[t][n] (+)= sum_k x[t][k] q[n][k] s[n][k / 32] for a 64-token x 128-row
-// tile per workgroup, one 32-wide k slice (one quant block) per step.
+// tile per workgroup, one 64-wide k stage (two quant blocks) per step.
 // Operands reach LDS by DMA (global_load_lds_dwordx4) into a ring of
-// kSlots slices, so three slices load while one is multiplied and no
-// register holds them in flight. Per slice: x_hi and x_lo (64 rows x 64 B
-// each; the four 16-byte granules of a row XOR-swizzled by (row >> 1) & 3
-// so that the A-fragment reads of 8 consecutive rows hit distinct banks),
-// the weight bytes (128 rows x 32 B for INT8, x 16 B for INT4; INT8 row
-// halves swizzled by (row >> 2) & 1) and the dword of each row's scales
-// that holds the slice's fp16 scale.
+// kStages stages, so one stage loads while one is multiplied and no
+// register holds them in flight. Per stage: x_hi and x_lo (64 rows x 128 B
+// each, whole 128-byte lines; the eight 16-byte granules of a row
+// XOR-swizzled by row & 7 so that the A-fragment reads of 8 consecutive rows
+// hit distinct banks), the weight bytes (128 rows x 64 B for INT8, x 32 B
+// for INT4; granules swizzled by (row >> 1) & 3 and (row >> 2) & 1) and the
+// dword of each row's scales holding the stage's two fp16 scales. A stage
+// costs the L2 one request per x row and limb, one per weight row and one
+// per scale dword: the L2 request rate, not its bandwidth, bounded the
+// 32-wide version.
 // Wave w multiplies all 64 tokens by rows [32 w, 32 w + 32): 4 x 2 tiles
-// of v_mfma_f32_16x16x32_f16, A = x limbs (hi and lo, two MFMAs per tile),
-// B = the codes, dequantised exactly into f16 from the wave's own rows;
-// then acc += s_n * D per tile. Lane layouts (checked on the device):
-// A[i][k]: lane i % 16 + 16 g holds k = 8 g .. 8 g + 7; B[k][n]: lane
-// n % 16 + 16 g the same k; D[i][n]: lane n + 16 (i / 4), element i % 4.
-constexpr int kSlots = 4;
-constexpr int kDmaPerWave = 4; // DMA instructions per wave per slice
+// of v_mfma_f32_16x16x32_f16 per block, A = x limbs (hi and lo, two MFMAs
+// per tile), B = the codes, dequantised exactly into f16 from the wave's
+// own rows; then acc += s_n * D per tile and block. Lane layouts (checked
+// on the device): A[i][k]: lane i % 16 + 16 g holds k = 8 g .. 8 g + 7;
+// B[k][n]: lane n % 16 + 16 g the same k; D[i][n]: lane n + 16 (i / 4),
+// element i % 4.
+constexpr int kStages = 3;
+constexpr int kDmaPerWave = 7; // DMA instructions per wave per stage
+constexpr int FS = 2 * FK;     // k per stage
 
 template <int QT> struct GemmSlot {
-    uint4 xh[FM_ROWS * 4];
-    uint4 xl[FM_ROWS * 4];
-    uint4 w[QT == 1 ? FN : 2 * FN];
+    uint4 xh[FM_ROWS * 8];
+    uint4 xl[FM_ROWS * 8];
+    uint4 w[QT == 1 ? 2 * FN : 4 * FN];
     uint32_t sc[FN];
 };
-
-// s_waitcnt with only vmcnt = n (expcnt and lgkmcnt left at their maxima).
-constexpr int vm_wait(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
-
-__device__ __forceinline__ void dma16(const void *src, void *lds)
-{
-    __builtin_amdgcn_global_load_lds(
-        (const __attribute__((address_space(1))) void *)src,
-        (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
-}
-
-__device__ __forceinline__ void dma4(const void *src, void *lds)
-{
-    __builtin_amdgcn_global_load_lds(
-        (const __attribute__((address_space(1))) void *)src,
-        (__attribute__((address_space(3))) void *)lds, 4, 0, 0);
-}
 
 // LDS address (byte offset) of a generic pointer into shared memory.
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
     return uint32_t(reinterpret_cast<uintptr_t>(
         (const __attribute__((address_space(3))) char *)(p)));
+}
+
+// LDS DMA of 16 (or 4) bytes per lane to lds + 16 (or 4) * lane, written as
+// asm: the compiler then neither tracks the DMA (it would wait for all of
+// it before any LDS read, as it cannot tell the ring slots apart) nor moves
+// memory operations across it. The LDS base must be wave-uniform.
+__device__ __forceinline__ void dma16(const void *src, const void *lds)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(m0)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void dma4(const void *src, const void *lds)
+{
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(src), "s"(m0)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) then s_barrier, as one compiler-level memory fence
+// (no workgroup fence: that would wait for every DMA in flight).
+template <int N> __device__ __forceinline__ void wait_dma_barrier()
+{
+    static_assert(N == 7, "the ring keeps one stage (seven DMA per wave) in flight");
+    asm volatile("s_waitcnt vmcnt(7)\n\ts_barrier" ::: "memory");
 }
 
 // Eight codes (k = 8 g .. 8 g + 7 of one row) as f16: INT8 from 8 bytes,
@@ -230,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
     GemmSegs segs)
 {
-    __shared__ GemmSlot<QT> slot0, slot1, slot2, slot3;
-    __shared__ uint4 junk[kWave];
+    __shared__ GemmSlot<QT> slot0, slot1, slot2;
+    __shared__ uint32_t junk[kWave];
     int seg = 0, tile = blockIdx.x;
     while (seg + 1 < segs.count && tile >= segs.tiles[seg])
         tile -= segs.tiles[seg++]; // workgroup-uniform
@@ -240,64 +258,70 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const int ldc = segs.ldc[seg];
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
-    const int k = w.cols, n_count = w.rows, blocks = k / FK;
+    const int k = w.cols, n_count = w.rows, stages = k / FS;
     const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
-    const int scale_words = blocks / 2; // dwords of scales per row
+    const int scale_words = k / FS; // one dword of scales per row and stage
 
-    // This lane's part of the wave's four DMA instructions per slice (all
-    // waves issue four, so one vmcnt value covers every wave): 0 = x_hi rows
-    // 16 wave + lane / 4, 1 = x_lo the same, 2 = weight rows (INT8: 32 per
-    // wave; INT4: 64 per wave for waves 0-1, the scale dwords of rows
-    // 64 (wave - 2) + lane for waves 2-3), 3 = INT8 scale dwords (waves 0-1)
-    // or a filler load into `junk`. Source pointers are at slice 0; a slice
-    // advances them by the slice's byte step.
-    const int xrow = 16 * wave + (lane >> 2);
-    const int xg = (lane & 3) ^ ((xrow >> 1) & 3);
-    const size_t xoff = size_t(min(t0 + xrow, t_count - 1)) * k + 8 * xg;
-    const char *src_xh = reinterpret_cast<const char *>(x_hi + xoff);
-    const char *src_xl = reinterpret_cast<const char *>(x_lo + xoff);
-    const char *src_w, *src_s;
-    int w_lds, s_lds;
-    bool w_is_scale, s_is_filler;
-    if (QT == 1) {
-        const int wrow = kWave * wave + lane; // waves 0-1
-        const int srow = kWave * (wave - 2) + lane; // waves 2-3
-        w_is_scale = wave >= 2;
-        const int r = w_is_scale ? srow : wrow;
-        src_w = w_is_scale ? reinterpret_cast<const char *>(w.scales) +
-                                 size_t(min(n0 + r, n_count - 1)) * scale_words * 4
-                           : reinterpret_cast<const char *>(w.data) +
-                                 size_t(min(n0 + r, n_count - 1)) * row_bytes;
-        w_lds = w_is_scale ? kWave * (wave - 2) : kWave * wave;
-        s_is_filler = true;
-        src_s = reinterpret_cast<const char *>(x_hi);
-        s_lds = 0;
-    } else {
-        const int wrow = 32 * wave + (lane >> 1);
-        const int gran = (lane & 1) ^ ((wrow >> 2) & 1);
-        w_is_scale = false;
-        src_w = reinterpret_cast<const char *>(w.data) +
-                size_t(min(n0 + wrow, n_count - 1)) * row_bytes + 16 * gran;
-        w_lds = kWave * wave;
-        s_is_filler = wave >= 2;
-        const int srow = kWave * wave + lane;
-        src_s = s_is_filler ? reinterpret_cast<const char *>(x_hi)
-                            : reinterpret_cast<const char *>(w.scales) +
-                                  size_t(min(n0 + srow, n_count - 1)) * scale_words * 4;
-        s_lds = kWave * wave;
-    }
-    auto issue = [&](GemmSlot<QT> &sl, int kb) {
-        kb = min(kb, blocks - 1); // past the end: reload the last slice
-        dma16(src_xh + size_t(kb) * (FK * 2), &sl.xh[kWave * wave]);
-        dma16(src_xl + size_t(kb) * (FK * 2), &sl.xl[kWave * wave]);
-        if (w_is_scale) // workgroup-uniform per wave
-            dma4(src_w + 4 * (kb >> 1), &sl.sc[w_lds]);
-        else
-            dma16(src_w + size_t(kb) * (QT == 1 ? 16 : 32), &sl.w[w_lds]);
-        if (s_is_filler)
-            dma16(src_s, &junk[0]);
-        else
-            dma4(src_s + 4 * (kb >> 1), &sl.sc[s_lds]);
+    // The wave's seven DMA instructions of a stage (every wave issues
+    // seven, so one vmcnt value covers every wave): x_hi and x_lo
+    // instructions 2 wave and 2 wave + 1 (8 rows each: row 8 i + lane / 8,
+    // granule lane % 8); INT8 weight instructions 2 wave and 2 wave + 1
+    // (16 rows each) and, for waves 0-1, the scale instructions; INT4:
+    // waves 0-1 the four weight instructions (32 rows each), waves 2-3 the
+    // two scale instructions; fillers into `junk` make up the seven. Source
+    // pointers are at stage 0.
+    // x rows of instructions 2 wave and 2 wave + 1
+    auto x_src = [&](const _Float16 *x, int i) {
+        const int row = 8 * i + (lane >> 3);
+        const int cg = (lane & 7) ^ (row & 7);
+        return reinterpret_cast<const char *>(x + size_t(min(t0 + row, t_count - 1)) * k +
+                                              8 * cg);
+    };
+    const int xi0 = 2 * wave, xi1 = 2 * wave + 1;
+    const char *const xh0 = x_src(x_hi, xi0), *const xh1 = x_src(x_hi, xi1);
+    const char *const xl0 = x_src(x_lo, xi0), *const xl1 = x_src(x_lo, xi1);
+    // weight rows: INT8 16 per instruction (instructions 2 wave, 2 wave + 1),
+    // INT4 32 per instruction (waves 0-1 only)
+    constexpr int W_ROWS = QT == 1 ? 32 : 16;
+    auto w_src = [&](int i) {
+        const int row = W_ROWS * i + (QT == 1 ? lane >> 1 : lane >> 2);
+        const int cg = QT == 1 ? (lane & 1) ^ ((row >> 2) & 1) : (lane & 3) ^ ((row >> 1) & 3);
+        return reinterpret_cast<const char *>(w.data) +
+               size_t(min(n0 + row, n_count - 1)) * row_bytes + 16 * cg;
+    };
+    const char *const w0 = w_src(xi0), *const w1 = w_src(xi1);
+    // scale dwords of rows 64 si + lane: INT8 waves 0-1, INT4 waves 2-3
+    const bool scales = QT == 1 ? wave >= 2 : wave < 2; // wave-uniform
+    const int si = QT == 1 ? wave - 2 : wave;
+    const char *const s0 = reinterpret_cast<const char *>(w.scales) +
+                           size_t(min(n0 + kWave * max(si, 0) + lane, n_count - 1)) *
+                               scale_words * 4;
+    const char *const filler = reinterpret_cast<const char *>(x_hi);
+    constexpr int W_STEP = QT == 1 ? FS / 2 : FS; // weight bytes per row and stage
+    auto issue = [&](GemmSlot<QT> &sl, int st) {
+        st = min(st, stages - 1); // past the end: reload the last stage
+        const size_t xs = size_t(st) * (FS * 2), ws = size_t(st) * W_STEP;
+        dma16(xh0 + xs, &sl.xh[kWave * xi0]);
+        dma16(xh1 + xs, &sl.xh[kWave * xi1]);
+        dma16(xl0 + xs, &sl.xl[kWave * xi0]);
+        dma16(xl1 + xs, &sl.xl[kWave * xi1]);
+        if (QT == 0) {
+            dma16(w0 + ws, &sl.w[kWave * xi0]);
+            dma16(w1 + ws, &sl.w[kWave * xi1]);
+            if (scales)
+                dma4(s0 + 4 * size_t(st), &sl.sc[kWave * si]);
+            else
+                dma4(filler, &junk[0]);
+        } else {
+            if (scales) {
+                dma4(s0 + 4 * size_t(st), &sl.sc[kWave * si]);
+                dma4(filler, &junk[0]);
+            } else {
+                dma16(w0 + ws, &sl.w[kWave * xi0]);
+                dma16(w1 + ws, &sl.w[kWave * xi1]);
+            }
+            dma4(filler, &junk[0]);
+        }
     };
 
     floatx4 acc[4][2];
@@ -307,114 +331,91 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
         for (int j = 0; j < 2; j++)
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const int g = lane >> 4, li = lane & 15;
-    // A fragments of rows 16 i + li (the swizzle (row >> 1) & 3 does not
-    // depend on i), B bytes and scale dwords of rows n = 32 wave + 16 j + li
-    // (the INT8 swizzle (n >> 2) & 1 does not depend on j): three base
-    // addresses per slot, constant offsets.
-    const uint32_t a_off = 16 * (4 * li + (g ^ ((li >> 1) & 3)));
     const int n_lane = 32 * wave + li;
-    const uint32_t b_off = QT == 1 ? 16 * n_lane + 4 * g
-                                   : 32 * n_lane + 16 * ((g >> 1) ^ ((li >> 2) & 1)) + 8 * (g & 1);
-    // The slot's operands, read in one asm block that ends with lgkmcnt(0):
-    // the reads are not matched against the DMA still in flight into the
-    // other ring slots (the compiler would wait for all of it), and every
-    // result depends on the wait. The caller's vmcnt wait and barrier have
-    // landed this slot.
-    auto compute = [&](const GemmSlot<QT> &sl, int kb) {
-        uint4 xa[4], xb[4];
-        uint2 raw[2];
-        uint32_t sw[2];
-        const uint32_t a_at = lds_addr(sl.xh) + a_off;
-        const uint32_t b_at = lds_addr(sl.w) + b_off;
-        const uint32_t s_at = lds_addr(sl.sc) + 4 * n_lane;
-        static_assert(sizeof(sl.xh) == 4096, "x_lo follows x_hi at 4 KB");
-        if (QT == 1) {
-            asm volatile("ds_read_b128 %0, %12\n"
-                         "ds_read_b128 %1, %12 offset:1024\n"
-                         "ds_read_b128 %2, %12 offset:2048\n"
-                         "ds_read_b128 %3, %12 offset:3072\n"
-                         "ds_read_b128 %4, %12 offset:4096\n"
-                         "ds_read_b128 %5, %12 offset:5120\n"
-                         "ds_read_b128 %6, %12 offset:6144\n"
-                         "ds_read_b128 %7, %12 offset:7168\n"
-                         "ds_read_b32 %8, %13\n"
-                         "ds_read_b32 %9, %13 offset:256\n"
-                         "ds_read_b32 %10, %14\n"
-                         "ds_read_b32 %11, %14 offset:64\n"
-                         "s_waitcnt lgkmcnt(0)"
-                         : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]),
-                           "=&v"(xb[0]), "=&v"(xb[1]), "=&v"(xb[2]), "=&v"(xb[3]),
-                           "=&v"(raw[0].x), "=&v"(raw[1].x), "=&v"(sw[0]), "=&v"(sw[1])
-                         : "v"(a_at), "v"(b_at), "v"(s_at)
-                         : "memory");
-            raw[0].y = raw[1].y = 0;
-        } else {
-            asm volatile("ds_read_b128 %0, %12\n"
-                         "ds_read_b128 %1, %12 offset:1024\n"
-                         "ds_read_b128 %2, %12 offset:2048\n"
-                         "ds_read_b128 %3, %12 offset:3072\n"
-                         "ds_read_b128 %4, %12 offset:4096\n"
-                         "ds_read_b128 %5, %12 offset:5120\n"
-                         "ds_read_b128 %6, %12 offset:6144\n"
-                         "ds_read_b128 %7, %12 offset:7168\n"
-                         "ds_read_b64 %8, %13\n"
-                         "ds_read_b64 %9, %13 offset:512\n"
-                         "ds_read_b32 %10, %14\n"
-                         "ds_read_b32 %11, %14 offset:64\n"
-                         "s_waitcnt lgkmcnt(0)"
-                         : "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]), "=&v"(xa[3]),
-                           "=&v"(xb[0]), "=&v"(xb[1]), "=&v"(xb[2]), "=&v"(xb[3]),
-                           "=&v"(raw[0]), "=&v"(raw[1]), "=&v"(sw[0]), "=&v"(sw[1])
-                         : "v"(a_at), "v"(b_at), "v"(s_at)
-                         : "memory");
-        }
-        half8 ah[4], al[4], b[2];
-        float sc[2];
+    // Fragment byte offsets in a slot (the swizzles depend on li only):
+    // A of row 16 i + li, block b: granule (4 b + g) ^ (li & 7) of the row;
+    // B of row n_lane + 16 j, block b.
+    auto a_off = [&](int b) { return 128 * li + 16 * ((4 * b + g) ^ (li & 7)); };
+    auto b_off = [&](int b) {
+        return QT == 1 ? 32 * n_lane + 16 * (b ^ ((li >> 2) & 1)) + 4 * g
+                       : 64 * n_lane + 16 * ((2 * b + (g >> 1)) ^ ((li >> 1) & 3)) + 8 * (g & 1);
+    };
+    auto stage_mma = [&](const GemmSlot<QT> &sl) {
+        const char *xh = reinterpret_cast<const char *>(sl.xh);
+        const char *xl = reinterpret_cast<const char *>(sl.xl);
+        const char *wb = reinterpret_cast<const char *>(sl.w);
+        uint4 xa[2][4], xb[2][4];
+        uint2 raw[2][2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ah[i] = __builtin_bit_cast(half8, xa[i]);
-            al[i] = __builtin_bit_cast(half8, xb[i]);
-        }
+        for (int b = 0; b < 2; b++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            b[j] = codes8<QT>(raw[j]);
-            sc[j] = half_bits_to_float(uint16_t(sw[j] >> (16 * (kb & 1))));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++) {
+                xa[b][i] = *reinterpret_cast<const uint4 *>(xh + 2048 * i + a_off(b));
+                xb[b][i] = *reinterpret_cast<const uint4 *>(xl + 2048 * i + a_off(b));
+            }
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                floatx4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    ah[i], b[j], floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], b[j], d, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    acc[i][j][v] = fmaf(sc[j], d[v], acc[i][j][v]);
+                const char *p = wb + b_off(b) + (QT == 1 ? 512 : 1024) * j;
+                raw[b][j] = QT == 1 ? make_uint2(*reinterpret_cast<const uint32_t *>(p), 0u)
+                                    : *reinterpret_cast<const uint2 *>(p);
             }
+        }
+        uint32_t sw[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            sw[j] = sl.sc[n_lane + 16 * j];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            half8 bq[2];
+            float sc[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                bq[j] = codes8<QT>(raw[b][j]);
+                sc[j] = half_bits_to_float(uint16_t(sw[j] >> (16 * b)));
+            }
+            // all eight x_hi products first, then the x_lo products into
+            // them, so no MFMA waits for the one just before it
+            floatx4 d[4][2];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    d[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, xa[b][i]), bq[j],
+                        floatx4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    d[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        __builtin_bit_cast(half8, xb[b][i]), bq[j], d[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[i][j][v] = fmaf(sc[j], d[i][j][v], acc[i][j][v]);
+        }
     };
-    // Slices kb + 1, kb + 2 stay in flight while slice kb is waited for;
-    // slice kb + 3 goes into the slot slice kb - 1 left.
-    // (a plain s_barrier: a workgroup fence would drain every DMA in flight;
-    // each wave's vmcnt wait has already landed its own part of slice kb)
-    auto step = [&](GemmSlot<QT> &cur, GemmSlot<QT> &next3, int kb) {
-        __builtin_amdgcn_s_waitcnt(vm_wait(2 * kDmaPerWave));
-        __builtin_amdgcn_s_barrier();
-        issue(next3, kb + 3);
-        compute(cur, kb);
+    // Stage s lives in slot s % 3. Step s: stage s landed in every wave
+    // (stage s + 1 stays in flight), and every wave is done with stage
+    // s - 1, whose slot takes stage s + 2.
+    auto step = [&](GemmSlot<QT> &cur, GemmSlot<QT> &free_slot, int st) {
+        wait_dma_barrier<kDmaPerWave>();
+        issue(free_slot, st + 2);
+        stage_mma(cur);
     };
     issue(slot0, 0);
     issue(slot1, 1);
-    issue(slot2, 2);
-    for (int kb = 0; kb < blocks; kb += kSlots) {
-        step(slot0, slot3, kb);
-        if (kb + 1 < blocks)
-            step(slot1, slot0, kb + 1);
-        if (kb + 2 < blocks)
-            step(slot2, slot1, kb + 2);
-        if (kb + 3 < blocks)
-            step(slot3, slot2, kb + 3);
+    for (int st = 0; st < stages; st += kStages) {
+        step(slot0, slot2, st);
+        if (st + 1 < stages)
+            step(slot1, slot0, st + 1);
+        if (st + 2 < stages)
+            step(slot2, slot1, st + 2);
     }
-    __builtin_amdgcn_s_waitcnt(vm_wait(0)); // no DMA outlives the workgroup
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // no DMA outlives the workgroup
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
