@@ -190,7 +190,7 @@ bool use_prefill_gemm(const nut_model &m, size_t count)
     if (m.path == 1 || count < kPrefillGemmMin)
         return false;
     for (const DeviceLayer &l : m.layers)
-        if (!prefill_gemm_supported(m.shape, l.view))
+        if (!prefill_gemm_supported(m.shape, l.view) || l.stage_scale[0] == nullptr)
             return false;
     return true;
 }
@@ -226,6 +226,7 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
     const size_t layer_elems = kv.layer_elements();
     for (size_t l = 0; l < m.layers.size(); l++) {
         const LayerView &w = m.layers[l].view;
+        const uint32_t *const *ss = m.layers[l].stage_scale;
         float *kc = kv.keys.as<float>() + l * layer_elems;
         float *vc = kv.values.as<float>() + l * layer_elems;
         const QMat *qkv_w[3] = {&w.query, &w.key, &w.value};
@@ -237,18 +238,18 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         const int gu_ld[2] = {s.ffn_dim, s.ffn_dim};
         launch_rmsnorm_rows(h, w.attention_norm, xh, xh + size_t(t) * s.dim, t, s.dim,
                             m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, qkv_c, qkv_ld, 3, false,
+        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, ss, qkv_c, qkv_ld, 3, false,
                           m.stream);
         launch_rope_store(q, k, v, m.rope.as<float2>(), kc, vc, s, t, 0, m.stream);
         launch_attention_prefill(q, kc, vc, ch, ch + size_t(t) * s.dim, s, t, 0, m.stream);
-        launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, &h, &s.dim, 1, true,
+        launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, ss + 3, &h, &s.dim, 1, true,
                           m.stream);
         launch_rmsnorm_rows(h, w.ffn_norm, xh, xh + size_t(t) * s.dim, t, s.dim, m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, gu_w, gu_c, gu_ld, 2, false,
+        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, gu_w, ss + 4, gu_c, gu_ld, 2, false,
                           m.stream);
         launch_silu_mul(g, u, xh, xh + size_t(t) * s.ffn_dim, size_t(t) * s.ffn_dim,
                         m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.ffn_dim, t, &wd, &h, &s.dim, 1, true,
+        launch_qgemm_rows(xh, xh + size_t(t) * s.ffn_dim, t, &wd, ss + 6, &h, &s.dim, 1, true,
                           m.stream);
     }
     hip_check(hipMemcpyAsync(m.hidden.get(), h + size_t(t - 1) * s.dim,
@@ -400,6 +401,24 @@ void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
     upload(norm_base + c.dim, ffn_norm, c.dim * sizeof(float));
     dl.view = LayerView{views[0], views[1], views[2], views[3], views[4],
                         views[5], views[6], norm_base, norm_base + c.dim};
+    dl.stage_scales.release();
+    for (int i = 0; i < 7; i++)
+        dl.stage_scale[i] = nullptr;
+    bool stages = true;
+    size_t words = 0;
+    for (int i = 0; i < 7; i++) {
+        stages = stages && views[i].block_size == 32 && views[i].cols % 64 == 0;
+        words += stages ? stage_scale_words(views[i]) : 0;
+    }
+    if (stages) {
+        dl.stage_scales.allocate(words * sizeof(uint32_t));
+        uint32_t *at = dl.stage_scales.as<uint32_t>();
+        for (int i = 0; i < 7; i++) {
+            launch_scales_by_stage(views[i], at, m.stream);
+            dl.stage_scale[i] = at;
+            at += stage_scale_words(views[i]);
+        }
+    }
     dl.storage_bytes = accounted + 2 * c.dim * sizeof(float);
     dl.set = true;
 }

@@ -18,6 +18,11 @@ struct DeviceLayer {
     // 32-wide blocks live in the model's arena instead.
     DeviceBuffer storage;
     LayerView view{};
+    // The prefill GEMM's stage-major copy of the seven matrices' scales
+    // (query, key, value, output, gate, up, down), when every matrix has
+    // 32-wide blocks in whole 64-wide stages.
+    DeviceBuffer stage_scales;
+    const uint32_t *stage_scale[7]{};
     bool in_arena = false;
     size_t storage_bytes = 0; // reference storage accounting
     bool set = false;

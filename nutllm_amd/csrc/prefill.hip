@@ -135,10 +135,25 @@ __device__ __forceinline__ uint32_t codes_from_pair(uint32_t pair, float bias)
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Stage-major scales: dword [st][row] = the fp16 scales of blocks 2 st and
+// 2 st + 1 of row `row` (the dword at row * stages + st of the row-major
+// scales).
+__global__ __launch_bounds__(kThreads) void scales_by_stage_kernel(const uint32_t *src,
+                                                                  uint32_t *dst, int rows,
+                                                                  int stages)
+{
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= size_t(rows) * stages)
+        return;
+    const int st = int(i / rows), row = int(i % rows);
+    dst[i] = src[size_t(row) * stages + st];
+}
+
 // Up to three matrices sharing X and k (Q/K/V, or gate/up) in one launch:
 // column tiles of FN outputs are numbered across the segments in order.
 struct GemmSegs {
     QMat w[3];
+    const uint32_t *st[3]; // stage-major scales (launch_scales_by_stage)
     float *c[3];
     int ldc[3];
     int tiles[3];
@@ -260,7 +275,6 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
     const int k = w.cols, n_count = w.rows, stages = k / FS;
     const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
-    const int scale_words = k / FS; // one dword of scales per row and stage
 
     // The wave's seven DMA instructions of a stage (every wave issues
     // seven, so one vmcnt value covers every wave): x_hi and x_lo
@@ -290,12 +304,13 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
                size_t(min(n0 + row, n_count - 1)) * row_bytes + 16 * cg;
     };
     const char *const w0 = w_src(xi0), *const w1 = w_src(xi1);
-    // scale dwords of rows 64 si + lane: INT8 waves 0-1, INT4 waves 2-3
+    // scale dwords of rows 64 si + lane (stage-major: consecutive rows are
+    // consecutive dwords): INT8 waves 0-1, INT4 waves 2-3
     const bool scales = QT == 1 ? wave >= 2 : wave < 2; // wave-uniform
     const int si = QT == 1 ? wave - 2 : wave;
-    const char *const s0 = reinterpret_cast<const char *>(w.scales) +
-                           size_t(min(n0 + kWave * max(si, 0) + lane, n_count - 1)) *
-                               scale_words * 4;
+    const char *const s0 = reinterpret_cast<const char *>(
+        segs.st[seg] + min(n0 + kWave * max(si, 0) + lane, n_count - 1));
+    const size_t s_step = size_t(n_count) * 4; // bytes per stage
     const char *const filler = reinterpret_cast<const char *>(x_hi);
     constexpr int W_STEP = QT == 1 ? FS / 2 : FS; // weight bytes per row and stage
     auto issue = [&](GemmSlot<QT> &sl, int st) {
@@ -309,12 +324,12 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
             dma16(w0 + ws, &sl.w[kWave * xi0]);
             dma16(w1 + ws, &sl.w[kWave * xi1]);
             if (scales)
-                dma4(s0 + 4 * size_t(st), &sl.sc[kWave * si]);
+                dma4(s0 + size_t(st) * s_step, &sl.sc[kWave * si]);
             else
                 dma4(filler, &junk[0]);
         } else {
             if (scales) {
-                dma4(s0 + 4 * size_t(st), &sl.sc[kWave * si]);
+                dma4(s0 + size_t(st) * s_step, &sl.sc[kWave * si]);
                 dma4(filler, &junk[0]);
             } else {
                 dma16(w0 + ws, &sl.w[kWave * xi0]);
@@ -611,9 +626,27 @@ void launch_rmsnorm_rows(const float *h, const float *w, _Float16 *out_hi,
     check_launch("prefill rmsnorm");
 }
 
+size_t stage_scale_words(const QMat &m)
+{
+    return size_t(m.rows) * size_t(m.cols / FS);
+}
+
+void launch_scales_by_stage(const QMat &m, uint32_t *dst, hipStream_t stream)
+{
+    require(m.block_size == 32 && m.cols % FS == 0, NUT_EINVAL,
+            "prefill gemm: stage scales need 32-wide blocks in whole 64-wide stages");
+    const size_t n = stage_scale_words(m);
+    hipLaunchKernelGGL(scales_by_stage_kernel, dim3(unsigned((n + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, stream,
+                       reinterpret_cast<const uint32_t *>(m.scales), dst, m.rows,
+                       m.cols / FS);
+    check_launch("prefill stage scales");
+}
+
 void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
-                       const QMat *const *w, float *const *c, const int *ldc, int count,
-                       bool add, hipStream_t stream)
+                       const QMat *const *w, const uint32_t *const *stage_scales,
+                       float *const *c, const int *ldc, int count, bool add,
+                       hipStream_t stream)
 {
     require(count >= 1 && count <= 3, NUT_EINVAL, "prefill gemm: 1 to 3 matrices");
     GemmSegs segs{};
@@ -621,7 +654,10 @@ void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
     for (int i = 0; i < count; i++) {
         require(w[i]->type == w[0]->type && w[i]->cols == w[0]->cols, NUT_EINVAL,
                 "prefill gemm: matrices differ in type or input size");
+        require(w[i]->cols % FS == 0 && stage_scales[i] != nullptr, NUT_EINVAL,
+                "prefill gemm: rows of whole 64-wide stages with stage-major scales");
         segs.w[i] = *w[i];
+        segs.st[i] = stage_scales[i];
         segs.c[i] = c[i];
         segs.ldc[i] = ldc[i];
         segs.tiles[i] = (w[i]->rows + FN - 1) / FN;

@@ -18,12 +18,18 @@ void launch_embed_rows(const float *embeddings, const int *tokens, float *h,
 // lo = f16(v - hi), [t][k] each.
 void launch_rmsnorm_rows(const float *h, const float *w, _Float16 *out_hi,
                          _Float16 *out_lo, int t_count, int dim, hipStream_t stream);
+// The prefill GEMM reads each matrix's fp16 scales stage-major: dword
+// [st][row] holds the scales of blocks 2 st and 2 st + 1 of the row
+// (stage_scale_words(m) dwords, built once per matrix).
+size_t stage_scale_words(const QMat &m);
+void launch_scales_by_stage(const QMat &m, uint32_t *dst, hipStream_t stream);
 // c_i[t][n] (= or +=) sum_k x[t][k] w_i[n][k] for `count` (1 to 3)
 // matrices of one type and input size, t < t_count, in one launch; x as
 // limbs of w.cols values per row, c_i rows ldc_i floats.
 void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
-                       const QMat *const *w, float *const *c, const int *ldc, int count,
-                       bool add, hipStream_t stream);
+                       const QMat *const *w, const uint32_t *const *stage_scales,
+                       float *const *c, const int *ldc, int count, bool add,
+                       hipStream_t stream);
 // RoPE of q rows and k rows at positions start + t; k and v rows into the
 // layer's cache.
 void launch_rope_store(float *q, const float *k, const float *v,
