@@ -213,6 +213,7 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         m.pf_ctx.allocate(rows * c.dim * sizeof(float));
         m.pf_g.allocate(rows * c.ffn_dim * sizeof(float));
         m.pf_u.allocate(rows * c.ffn_dim * sizeof(float));
+        m.pf_kv.allocate(4 * prefill_kv_limb_elems(s) * sizeof(_Float16));
     }
     const int t = int(count);
     // GEMM inputs as f16 limbs (hi rows, then lo rows): the normalised x and
@@ -241,7 +242,8 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, ss, qkv_c, qkv_ld, 3, false,
                           m.stream);
         launch_rope_store(q, k, v, m.rope.as<float2>(), kc, vc, s, t, 0, m.stream);
-        launch_attention_prefill(q, kc, vc, ch, ch + size_t(t) * s.dim, s, t, 0, m.stream);
+        launch_attention_prefill(q, kc, vc, m.pf_kv.as<_Float16>(), ch, ch + size_t(t) * s.dim,
+                                 s, t, m.stream);
         launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, ss + 3, &h, &s.dim, 1, true,
                           m.stream);
         launch_rmsnorm_rows(h, w.ffn_norm, xh, xh + size_t(t) * s.dim, t, s.dim, m.stream);

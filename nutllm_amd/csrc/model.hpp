@@ -77,6 +77,7 @@ struct nut_model {
     nut::DeviceBuffer exchange, token_error, timeline;
     // Prefill GEMM path: activations of a whole prompt, max_seq rows each.
     nut::DeviceBuffer pf_h, pf_x, pf_q, pf_k, pf_v, pf_ctx, pf_g, pf_u;
+    nut::DeviceBuffer pf_kv; // the batch's K and V as f16 limbs (prefill attention)
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
     int timeline_wgs = 0;        // workgroups it covers
     unsigned launch_count = 0;

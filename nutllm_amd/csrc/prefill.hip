@@ -463,27 +463,65 @@ void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
 }
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
-// start + t attend to cache positions 0 .. start + t, in 64-key tiles.
+// t attend to cache positions 0 .. t, in 64-key tiles.
 constexpr int AQ = 64, AK = 64;
 
-// On v_mfma_f32_16x16x4f32 (fp32 operands, as the reference's
-// arithmetic): one workgroup per (head, 64-query tile);
-// wave w owns queries 16 w .. 16 w + 15. Per 64-key tile (K and V in LDS):
-// S = Q K^T as 4 x (HD / 4) MFMAs with Q in registers, the online softmax
-// on S in registers (a query row lives in one 16-lane DPP row), P through
-// LDS into the A layout, then O += P V as (HD / 16) x 16 MFMAs. Lane
-// layouts of the 16x16x4 MFMA: A[i][k] in lane i + 16 k, B[k][n] in lane
-// n + 16 k, D[i][n] in lane n + 16 (i / 4), element i % 4.
+// Positions of the K/V limb buffers: max_seq rounded up to whole key tiles.
+int kv_limb_rows(const DecodeShape &s) { return (s.max_seq + AK - 1) / AK * AK; }
+
+// K and V of the batch's positions as f16 limbs (hi = f16(v), lo =
+// f16(v - hi)), written once per layer for the attention below: K as
+// [kv_head][pos][HD], V transposed as [kv_head][HD][pos], positions padded
+// to a multiple of 64 with zeros (a masked key then has an exact zero
+// weight times a finite value). One workgroup per (kv head, 64 positions);
+// the V tile is transposed through LDS so that reads and writes stay
+// coalesced.
 template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
-    const float *q, const float *k_cache, const float *v_cache, _Float16 *ctx_hi,
-    _Float16 *ctx_lo, int t_count, int heads, int kv_heads, int max_seq, int start,
-    float scale)
+__global__ __launch_bounds__(kThreads) void kv_limbs_kernel(
+    const float *k_cache, const float *v_cache, int max_seq, int t_count, int t_pad,
+    _Float16 *k_hi, _Float16 *k_lo, _Float16 *vt_hi, _Float16 *vt_lo)
 {
-    constexpr int KP = HD + 4, VP = HD + 16, PP = AK + 4;
-    __shared__ float ks[AK][KP];
-    __shared__ float vs[AK][VP];
-    __shared__ float ps[4][16][PP];
+    __shared__ float tile[AK][HD + 1];
+    const int kvh = blockIdx.x, p0 = blockIdx.y * AK;
+    const float *kc = k_cache + size_t(kvh) * max_seq * HD;
+    const float *vc = v_cache + size_t(kvh) * max_seq * HD;
+    for (int e = threadIdx.x; e < AK * HD; e += kThreads) {
+        const int p = e / HD, d = e % HD;
+        const bool in = p0 + p < t_count;
+        const float kv = in ? kc[size_t(p0 + p) * HD + d] : 0.0f;
+        const size_t at = (size_t(kvh) * t_pad + p0 + p) * HD + d;
+        put_limbs(k_hi, k_lo, at, kv);
+        tile[p][d] = in ? vc[size_t(p0 + p) * HD + d] : 0.0f;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < AK * HD; e += kThreads) {
+        const int d = e / AK, p = e % AK;
+        put_limbs(vt_hi, vt_lo, (size_t(kvh) * HD + d) * t_pad + p0 + p, tile[p][d]);
+    }
+}
+
+// On v_mfma_f32_16x16x32_f16 with operands as f16 limbs: every product a b
+// is a_hi b_hi + a_hi b_lo + a_lo b_hi (three MFMAs; the dropped a_lo b_lo
+// is below 2^-22 of a b), so S and P V carry fp32-level precision at the
+// f16 matrix rate. One workgroup per (head, 64-query tile); wave w owns
+// queries 16 w .. 16 w + 15 and holds their Q limbs in registers. Per
+// 64-key tile (K limbs [key][d] and V limbs [d][key] in LDS): S = Q K^T,
+// the online softmax on S in registers (a query row lives in one 16-lane
+// DPP row), P as limbs through LDS into the A layout, then O += P V. Lane
+// layouts (checked on the device): A[i][k]: lane i % 16 + 16 g holds k =
+// 8 g .. 8 g + 7; B[k][n]: lane n % 16 + 16 g the same k; D[i][n]: lane
+// n + 16 (i / 4), element i % 4.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void attention_prefill_f16(
+    const float *q, const _Float16 *k_hi, const _Float16 *k_lo, const _Float16 *vt_hi,
+    const _Float16 *vt_lo, _Float16 *ctx_hi, _Float16 *ctx_lo, int t_count, int t_pad,
+    int heads, int kv_heads, float scale)
+{
+    constexpr int KP = HD + 8, VP = AK + 8, PP = AK + 8; // rows padded by 16 bytes
+    constexpr int KB = HD / 32;                            // 32-wide k blocks of a head
+    __shared__ __attribute__((aligned(16))) _Float16 ksh[AK][KP], ksl[AK][KP];
+    __shared__ __attribute__((aligned(16))) _Float16 vsh[HD][VP], vsl[HD][VP];
+    __shared__ __attribute__((aligned(16))) _Float16 psh[4][16][PP], psl[4][16][PP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     // heads vary fastest and the longest query tiles (the most key tiles
@@ -491,23 +529,29 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
     const int head = blockIdx.x, g = head / (heads / kv_heads);
     const int t0 = (gridDim.y - 1 - blockIdx.y) * AQ;
     const int dim = heads * HD;
-    // Q fragments of this wave's rows: A[i = li][k = 4 s + lg]
-    float qa[HD / 4];
+    // Q limbs of this wave's rows: A[i = li][k = 32 kb + 8 lg + j]
+    half8 qh[KB], ql[KB];
     {
         const int t = t0 + 16 * wave + li;
         const float *qr = q + size_t(min(t, t_count - 1)) * dim + head * HD;
 #pragma unroll
-        for (int st = 0; st < HD / 4; st++)
-            qa[st] = t < t_count ? qr[4 * st + lg] : 0.0f;
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float x = t < t_count ? qr[32 * kb + 8 * lg + j] : 0.0f;
+                const _Float16 hi = (_Float16)x;
+                qh[kb][j] = hi;
+                ql[kb][j] = (_Float16)(x - (float)hi);
+            }
     }
-    const float *kg = k_cache + size_t(g) * max_seq * HD;
-    const float *vg = v_cache + size_t(g) * max_seq * HD;
-    const int last = min(start + t0 + AQ - 1, start + t_count - 1);
+    const _Float16 *kgh = k_hi + size_t(g) * t_pad * HD, *kgl = k_lo + size_t(g) * t_pad * HD;
+    const _Float16 *vgh = vt_hi + size_t(g) * HD * t_pad, *vgl = vt_lo + size_t(g) * HD * t_pad;
+    const int last = min(t0 + AQ - 1, t_count - 1);
     // rows of this lane: r = 4 lg + v (v < 4) of the wave's 16
     int qpos[4];
 #pragma unroll
     for (int v = 0; v < 4; v++)
-        qpos[v] = start + t0 + 16 * wave + 4 * lg + v;
+        qpos[v] = t0 + 16 * wave + 4 * lg + v;
     float m[4], l[4];
     floatx4 o[HD / 16];
 #pragma unroll
@@ -518,29 +562,41 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
 #pragma unroll
     for (int dt = 0; dt < HD / 16; dt++)
         o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma3 = [](const half8 &ah, const half8 &al, const half8 &bh, const half8 &bl,
+                   floatx4 acc) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+    };
     for (int p0 = 0; p0 <= last; p0 += AK) {
         __syncthreads(); // previous tile's readers are done
-        for (int e = tid; e < AK * HD / 4; e += kThreads) {
-            const int j = e / (HD / 4), d4 = e % (HD / 4);
-            const bool in = p0 + j <= last;
-            const float4 kv = in ? reinterpret_cast<const float4 *>(kg + size_t(p0 + j) * HD)[d4]
-                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float4 vv = in ? reinterpret_cast<const float4 *>(vg + size_t(p0 + j) * HD)[d4]
-                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            *reinterpret_cast<float4 *>(&ks[j][4 * d4]) = kv;
-            *reinterpret_cast<float4 *>(&vs[j][4 * d4]) = vv;
+        // K tile rows p0 .. p0 + 63 (16-byte pieces), V^T tile [d][p0 ..]
+        for (int e = tid; e < AK * HD / 8; e += kThreads) {
+            const int j = e / (HD / 8), c8 = e % (HD / 8);
+            const size_t at = size_t(p0 + j) * HD + 8 * c8;
+            *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgh + at);
+            *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgl + at);
+        }
+        for (int e = tid; e < HD * AK / 8; e += kThreads) {
+            const int d = e / (AK / 8), c8 = e % (AK / 8);
+            const size_t at = size_t(d) * t_pad + p0 + 8 * c8;
+            *reinterpret_cast<uint4 *>(&vsh[d][8 * c8]) = *reinterpret_cast<const uint4 *>(vgh + at);
+            *reinterpret_cast<uint4 *>(&vsl[d][8 * c8]) = *reinterpret_cast<const uint4 *>(vgl + at);
         }
         __syncthreads();
         // S tiles: keys 16 nt + li, rows 4 lg + v
         floatx4 sc[4];
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
+        for (int nt = 0; nt < 4; nt++)
             sc[nt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int st = 0; st < HD / 4; st++)
-                sc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                    qa[st], ks[16 * nt + li][4 * st + lg], sc[nt], 0, 0, 0);
-        }
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                const half8 bh = *reinterpret_cast<const half8 *>(&ksh[16 * nt + li][32 * kb + 8 * lg]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&ksl[16 * nt + li][32 * kb + 8 * lg]);
+                sc[nt] = mma3(qh[kb], ql[kb], bh, bl, sc[nt]);
+            }
         float corr[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
@@ -560,7 +616,9 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
 #pragma unroll
             for (int nt = 0; nt < 4; nt++) {
                 const float e = sc[nt][v] == -INFINITY ? 0.0f : expf(sc[nt][v] - mn);
-                ps[wave][4 * lg + v][16 * nt + li] = e;
+                const _Float16 hi = (_Float16)e;
+                psh[wave][4 * lg + v][16 * nt + li] = hi;
+                psl[wave][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
                 sum += e;
             }
             l[v] = l[v] * corr[v] + row16_sum(sum);
@@ -571,16 +629,19 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_mfma(
 #pragma unroll
             for (int v = 0; v < 4; v++)
                 o[dt][v] *= corr[v];
-        // ps rows of this wave are written by this wave only
+        // P rows of this wave are written and read by this wave only
         __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): LDS writes done
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int st = 0; st < AK / 4; st++) {
-            const float pa = ps[wave][li][4 * st + lg];
+        for (int kb = 0; kb < AK / 32; kb++) {
+            const half8 ah = *reinterpret_cast<const half8 *>(&psh[wave][li][32 * kb + 8 * lg]);
+            const half8 al = *reinterpret_cast<const half8 *>(&psl[wave][li][32 * kb + 8 * lg]);
 #pragma unroll
-            for (int dt = 0; dt < HD / 16; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                    pa, vs[4 * st + lg][16 * dt + li], o[dt], 0, 0, 0);
+            for (int dt = 0; dt < HD / 16; dt++) {
+                const half8 bh = *reinterpret_cast<const half8 *>(&vsh[16 * dt + li][32 * kb + 8 * lg]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&vsl[16 * dt + li][32 * kb + 8 * lg]);
+                o[dt] = mma3(ah, al, bh, bl, o[dt]);
+            }
         }
     }
 #pragma unroll
@@ -680,20 +741,34 @@ void launch_rope_store(float *q, const float *k, const float *v,
     check_launch("prefill rope");
 }
 
+size_t prefill_kv_limb_elems(const DecodeShape &s)
+{
+    return size_t(s.kv_heads) * kv_limb_rows(s) * s.head_dim;
+}
+
 void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, _Float16 *ctx_hi, _Float16 *ctx_lo,
-                              const DecodeShape &s, int t_count, int start,
+                              const float *v_cache, _Float16 *kv_limbs, _Float16 *ctx_hi,
+                              _Float16 *ctx_lo, const DecodeShape &s, int t_count,
                               hipStream_t stream)
 {
-    const dim3 grid(s.heads, (t_count + AQ - 1) / AQ);
-    if (s.head_dim == 128)
-        hipLaunchKernelGGL(attention_prefill_mfma<128>, grid, dim3(kThreads), 0,
-                           stream, q, k_cache, v_cache, ctx_hi, ctx_lo, t_count, s.heads,
-                           s.kv_heads, s.max_seq, start, s.attn_scale);
-    else
-        hipLaunchKernelGGL(attention_prefill_mfma<64>, grid, dim3(kThreads), 0,
-                           stream, q, k_cache, v_cache, ctx_hi, ctx_lo, t_count, s.heads,
-                           s.kv_heads, s.max_seq, start, s.attn_scale);
+    const int t_pad = (t_count + AK - 1) / AK * AK;
+    require(t_pad <= kv_limb_rows(s), NUT_EINVAL, "prefill attention: prompt too long");
+    const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
+    _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
+    const dim3 kv_grid(s.kv_heads, t_pad / AK), grid(s.heads, t_pad / AQ);
+    if (s.head_dim == 128) {
+        hipLaunchKernelGGL(kv_limbs_kernel<128>, kv_grid, dim3(kThreads), 0, stream, k_cache,
+                           v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
+        hipLaunchKernelGGL(attention_prefill_f16<128>, grid, dim3(kThreads), 0, stream, q,
+                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad, s.heads,
+                           s.kv_heads, s.attn_scale);
+    } else {
+        hipLaunchKernelGGL(kv_limbs_kernel<64>, kv_grid, dim3(kThreads), 0, stream, k_cache,
+                           v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
+        hipLaunchKernelGGL(attention_prefill_f16<64>, grid, dim3(kThreads), 0, stream, q,
+                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad, s.heads,
+                           s.kv_heads, s.attn_scale);
+    }
     check_launch("prefill attention");
 }
 

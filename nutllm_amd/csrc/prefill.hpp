@@ -36,11 +36,13 @@ void launch_rope_store(float *q, const float *k, const float *v,
                        const float2 *rope, float *k_cache, float *v_cache,
                        const DecodeShape &s, int t_count, int start,
                        hipStream_t stream);
-// Causal attention of the t_count queries over cache positions
-// 0 .. start + t.
+// Causal attention of the t_count queries (positions 0 .. t_count - 1) over
+// cache positions 0 .. t; kv_limbs is a workspace of
+// 4 * prefill_kv_limb_elems(s) f16 (the batch's K and V as f16 limbs).
+size_t prefill_kv_limb_elems(const DecodeShape &s);
 void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, _Float16 *ctx_hi, _Float16 *ctx_lo,
-                              const DecodeShape &s, int t_count, int start,
+                              const float *v_cache, _Float16 *kv_limbs, _Float16 *ctx_hi,
+                              _Float16 *ctx_lo, const DecodeShape &s, int t_count,
                               hipStream_t stream);
 void launch_silu_mul(const float *g, const float *u, _Float16 *act_hi,
                      _Float16 *act_lo, size_t n, hipStream_t stream);
