@@ -547,6 +547,9 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_f16(
     const _Float16 *kgh = k_hi + size_t(g) * t_pad * HD, *kgl = k_lo + size_t(g) * t_pad * HD;
     const _Float16 *vgh = vt_hi + size_t(g) * HD * t_pad, *vgl = vt_lo + size_t(g) * HD * t_pad;
     const int last = min(t0 + AQ - 1, t_count - 1);
+    // softmax in base 2: scores scaled by scale * log2(e), weights
+    // exp2(s - m) with the hardware exp2 (about 1 ulp)
+    const float scale2 = scale * 1.4426950408889634f;
     // rows of this lane: r = 4 lg + v (v < 4) of the wave's 16
     int qpos[4];
 #pragma unroll
@@ -604,18 +607,18 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_f16(
 #pragma unroll
             for (int nt = 0; nt < 4; nt++) {
                 const int kpos = p0 + 16 * nt + li;
-                const float x = kpos <= qpos[v] ? sc[nt][v] * scale : -INFINITY;
+                const float x = kpos <= qpos[v] ? sc[nt][v] * scale2 : -INFINITY;
                 sc[nt][v] = x;
                 tmax = fmaxf(tmax, x);
             }
             tmax = row16_max(tmax);
             const float mn = fmaxf(m[v], tmax);
             // rows past t_count (and fully masked tiles) keep m = -inf
-            corr[v] = mn == -INFINITY ? 1.0f : expf(m[v] - mn);
+            corr[v] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[v] - mn);
             float sum = 0.0f;
 #pragma unroll
             for (int nt = 0; nt < 4; nt++) {
-                const float e = sc[nt][v] == -INFINITY ? 0.0f : expf(sc[nt][v] - mn);
+                const float e = sc[nt][v] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[nt][v] - mn);
                 const _Float16 hi = (_Float16)e;
                 psh[wave][4 * lg + v][16 * nt + li] = hi;
                 psl[wave][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
