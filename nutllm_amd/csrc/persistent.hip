@@ -200,15 +200,6 @@ __device__ __forceinline__ int swz(int i)
     return (b << 5) | (((q + b) & 7) << 2) | (i & 3);
 }
 
-__device__ __forceinline__ void load_x_block(const float *xs, int b,
-                                             float4 (&xq)[8])
-{
-    const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
-#pragma unroll
-    for (int q = 0; q < 8; q++)
-        xq[q] = base[(q + b) & 7];
-}
-
 // Workgroup sum of per-thread values; every thread gets the total.
 __device__ __forceinline__ float wg_sum(float v, float *red)
 {
@@ -225,6 +216,7 @@ __device__ __forceinline__ float wg_sum(float v, float *red)
     return total;
 }
 
+// Block sums of x (swizzled), for the offset-binary float dots.
 __device__ void block_sums(const float *xs, float *xsum, int n)
 {
     for (int b = threadIdx.x; b < n / 32; b += kThreads) {
@@ -236,6 +228,83 @@ __device__ void block_sums(const float *xs, float *xsum, int n)
         xsum[b] = s;
     }
     __syncthreads();
+}
+
+// x of a dim-sized phase as integer digits for the dot instructions. Per
+// 32-element block b with m = max |x_k|: X_k = rint(x_k * kLimbRange / m),
+// so x_k = xsc[b] * X_k to 2^-23.7 m, and X_k is written as signed digits,
+// six of 4 bits (INT4 rows, v_dot8_i32_i4) or three of 8 bits (INT8 rows,
+// v_dot4_i32_i8): X_k = sum_d digit_d 16^d (or 256^d). The digits come from
+// the offset form: for INT4, X + 0x888888 has hex digits e_d in 0..15 and
+// digit_d = e_d - 8, which as a 4-bit two's-complement field is e_d ^ 8, so
+// (X + 0x888888) ^ 0x888888 holds the six digits as nibbles (|X| <= 7e6
+// keeps X + 0x888888 in 0..2^24); INT8 likewise with 0x808080. Block b's
+// kLimbWords words at xl + kLimbStride * b: INT4 word 4 d + j holds digit d
+// of elements 8 j .. 8 j + 7 (nibble t = element 8 j + t, the weights'
+// nibble order); INT8 word 8 d + j digit d of elements 4 j .. 4 j + 3. A
+// NaN or infinity in a block makes xsc[b] NaN.
+constexpr float kLimbRange = 7.0e6f;
+constexpr int kLimbWords = 24;
+constexpr int kLimbStride = 28; // words; lanes b .. b + 15 hit distinct banks
+
+// Digits of quartet q (elements 4 q .. 4 q + 3) of block b, from the lane
+// holding it; the block's eight quartets sit in lanes 8 k .. 8 k + 7 of one
+// wave (DPP reduces the block maximum), all lanes of the wave take part.
+template <int QT>
+__device__ __forceinline__ void quartet_digits(float4 v, int b, int q, uint32_t *xl,
+                                               float *xsc)
+{
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    float poison = ((v.x + v.y) + (v.z + v.w)) * 0.0f; // NaN for NaN or inf
+    mx = fmaxf(mx, dpp<kDppQuadSwap1>(mx, 0.0f));
+    mx = fmaxf(mx, dpp<kDppQuadSwap2>(mx, 0.0f));
+    mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx, 0.0f));
+    poison += dpp<kDppQuadSwap1>(poison, 0.0f);
+    poison += dpp<kDppQuadSwap2>(poison, 0.0f);
+    poison += dpp<kDppRowHalfMirror>(poison, 0.0f);
+    // r within an ulp of kLimbRange / mx: x_k = xsc X_k holds to 2^-23
+    const float r = mx > 0.0f ? kLimbRange * __builtin_amdgcn_rcpf(mx) : 0.0f;
+    if (q == 0)
+        xsc[b] = mx * (1.0f / kLimbRange) + poison;
+    // X + offset in one FMA (exact below 2^24 up to its rounding) and one
+    // conversion: v_cvt_rpi_i32_f32 is floor(v + 0.5)
+    constexpr uint32_t kOff = QT == 1 ? 0x888888u : 0x808080u;
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        int c;
+        asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(c) : "v"(fmaf(xv[k], r, float(kOff))));
+        y[k] = uint32_t(c) ^ kOff;
+    }
+    // P[i] = byte i of y[0..3], one per byte
+    const uint32_t a01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+    const uint32_t a23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+    const uint32_t c01 = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0602u);
+    const uint32_t c23 = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0602u);
+    const uint32_t P[3] = {__builtin_amdgcn_perm(a23, a01, 0x05040100u),
+                           __builtin_amdgcn_perm(a23, a01, 0x07060302u),
+                           __builtin_amdgcn_perm(c23, c01, 0x05040100u)};
+    uint32_t *blk = xl + kLimbStride * b;
+    if (QT == 1) {
+        // digit 2 i is the low nibble of byte i, 2 i + 1 the high one; the
+        // quartet is nibbles 4 (q & 1) .. 4 (q & 1) + 3 of word (d, q >> 1)
+        uint16_t *half = reinterpret_cast<uint16_t *>(blk + (q >> 1)) + (q & 1);
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+#pragma unroll
+            for (int hi = 0; hi < 2; hi++) {
+                const uint32_t n = (hi ? P[i] >> 4 : P[i]) & 0x0f0f0f0fu;
+                const uint32_t m = n | (n >> 4); // nibble pairs in bytes 0, 2
+                half[2 * 4 * (2 * i + hi)] =
+                    uint16_t(__builtin_amdgcn_perm(0u, m, 0x0c0c0200u));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            blk[8 * i + q] = P[i];
+    }
 }
 
 // This thread's elements i = threadIdx.x + kThreads * u of an N-vector in
@@ -267,19 +336,19 @@ template <int N> struct Slice {
     }
 };
 
-// xs (swizzled) = src * scale * w, plus block sums; ends with a barrier.
-template <int N>
-__device__ void stage_x(const float *src, const Slice<N> &w, float scale,
-                        float *xs, float *xsum)
+// Digits (quartet_digits) of x = src * scale * w for a dim of 4 kThreads:
+// thread t takes elements 4 t .. 4 t + 3, w holding its four weights.
+// Ends with a barrier.
+template <int QT, int N>
+__device__ void stage_x(const float *src, float4 w, float scale, uint32_t *xl,
+                        float *xsc)
 {
-#pragma unroll
-    for (int u = 0; u < Slice<N>::PER; u++) {
-        const int i = threadIdx.x + u * kThreads;
-        if (i < N)
-            xs[swz(i)] = src[i] * scale * w.v[u];
-    }
+    static_assert(N == 4 * kThreads, "one quartet per thread");
+    const float4 h = reinterpret_cast<const float4 *>(src)[threadIdx.x];
+    const float4 x = make_float4(h.x * scale * w.x, h.y * scale * w.y, h.z * scale * w.z,
+                                 h.w * scale * w.w);
+    quartet_digits<QT>(x, threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
     __syncthreads();
-    block_sums(xs, xsum, N);
 }
 
 __device__ __forceinline__ float rms_scale(float squares, int n)
@@ -385,68 +454,15 @@ __device__ __forceinline__ float dot_block_int8(const uint4 &w0,
     return a0 + a1;
 }
 
-// Block b of a staged row (data in LDS) dotted with x quads, minus the
-// offset-binary bias, times the block's fp16 scale.
-template <int QT>
-__device__ __forceinline__ float block_term(const uint8_t *row,
-                                           const uint16_t *scales, int b,
-                                           const float4 (&xq)[8], float xsum)
-{
-    float d;
-    if (QT == 1) {
-        d = dot_block_int4(reinterpret_cast<const uint4 *>(row)[b], xq) -
-            8.0f * xsum;
-    } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
-        d = dot_block_int8(p[0], p[1], xq) - 128.0f * xsum;
-    }
-    return half_bits_to_float(scales[b]) * d;
-}
-
-// x of one phase held in registers, lane's blocks b = lane + 64 j.
-template <int CPL> struct XRegs {
-    float4 q[CPL][8];
-    float sum[CPL];
-};
-
-template <int CPL>
-__device__ __forceinline__ void load_x(XRegs<CPL> &x, const float *xs,
-                                       const float *xsum, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks) {
-            load_x_block(xs, b, x.q[j]);
-            x.sum[j] = xsum[b];
-        }
-    }
-}
-
-// Wave dot product of a staged row with x in registers; all lanes get it.
+// Wave dot product of a staged row with x (swizzled floats in LDS, block
+// sums xsum): per block, offset-binary codes against x minus the bias times
+// the block sum, times the block's fp16 scale. Used where x is ffn-sized:
+// staging its digits would cost more than the float dot.
 template <int QT, int CPL>
-__device__ __forceinline__ float row_dot(const uint8_t *row,
-                                         const uint16_t *scales,
-                                         const XRegs<CPL> &x, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks)
-            acc += block_term<QT>(row, scales, b, x.q[j], x.sum[j]);
-    }
-    return wave_total(acc);
-}
-
-// As row_dot, reading x from LDS (rows swept once per wave).
-template <int QT, int CPL>
-__device__ __forceinline__ float row_dot_lds(const uint8_t *row,
-                                             const uint16_t *scales,
-                                             const float *xs,
-                                             const float *xsum, int blocks)
+__device__ __forceinline__ float row_dot_floats(const uint8_t *row,
+                                                const uint16_t *scales,
+                                                const float *xs,
+                                                const float *xsum, int blocks)
 {
     const int lane = threadIdx.x & (kWave - 1);
     float acc = 0.0f;
@@ -455,8 +471,133 @@ __device__ __forceinline__ float row_dot_lds(const uint8_t *row,
         const int b = lane + kWave * j;
         if (b < blocks) {
             float4 xq[8];
-            load_x_block(xs, b, xq);
-            acc += block_term<QT>(row, scales, b, xq, xsum[b]);
+            const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                xq[q] = base[(q + b) & 7];
+            float d;
+            if (QT == 1) {
+                d = dot_block_int4(reinterpret_cast<const uint4 *>(row)[b], xq) -
+                    8.0f * xsum[b];
+            } else {
+                const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
+                d = dot_block_int8(p[0], p[1], xq) - 128.0f * xsum[b];
+            }
+            acc += half_bits_to_float(scales[b]) * d;
+        }
+    }
+    return wave_total(acc);
+}
+
+// One block of a staged row (its two's-complement codes as stored) dotted
+// with the block's digits, exactly in integers per digit: every digit sum
+// is at most 32 * 7 * 8 (INT4) or 32 * 127 * 128 (INT8) in magnitude, and
+// the weighted sums below stay inside int32; the one or two conversions to
+// float round once each.
+template <int QT>
+__device__ __forceinline__ float dot_block_digits(const uint8_t *row, int b,
+                                                  const uint4 (&d)[6])
+{
+    if (QT == 1) {
+        const uint4 w = reinterpret_cast<const uint4 *>(row)[b];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        int acc[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) {
+            const uint32_t ds[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
+            acc[i] = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i] = __builtin_amdgcn_sdot8(int(ws[j]), int(ds[j]), acc[i], false);
+        }
+        const int lo = acc[0] + acc[1] * 16 + acc[2] * 256;
+        const int hi = acc[3] + acc[4] * 16 + acc[5] * 256;
+        return fmaf(float(hi), 4096.0f, float(lo));
+    } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
+        const uint4 w0 = p[0], w1 = p[1];
+        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        int acc[3];
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const uint32_t ds[8] = {d[2 * i].x, d[2 * i].y, d[2 * i].z, d[2 * i].w,
+                                    d[2 * i + 1].x, d[2 * i + 1].y, d[2 * i + 1].z,
+                                    d[2 * i + 1].w};
+            acc[i] = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc[i] = __builtin_amdgcn_sdot4(int(ws[j]), int(ds[j]), acc[i], false);
+        }
+        const int lo = acc[0] + acc[1] * 256;
+        return fmaf(float(acc[2]), 65536.0f, float(lo));
+    }
+}
+
+__device__ __forceinline__ void load_digits(const uint32_t *xl, int b, uint4 (&d)[6])
+{
+    const uint4 *p = reinterpret_cast<const uint4 *>(xl + kLimbStride * b);
+#pragma unroll
+    for (int i = 0; i < 6; i++)
+        d[i] = p[i];
+}
+
+// x of one phase held in registers as digits, lane's blocks b = lane + 64 j.
+template <int CPL> struct XDigits {
+    uint4 d[CPL][6];
+    float sc[CPL];
+};
+
+template <int CPL>
+__device__ __forceinline__ void load_x(XDigits<CPL> &x, const uint32_t *xl,
+                                       const float *xsc, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks) {
+            load_digits(xl, b, x.d[j]);
+            x.sc[j] = xsc[b];
+        }
+    }
+}
+
+// Wave dot product of a staged row with x in registers; all lanes get it.
+// Block b contributes (its fp16 scale) * xsc[b] * (integer block dot).
+template <int QT, int CPL>
+__device__ __forceinline__ float row_dot(const uint8_t *row,
+                                         const uint16_t *scales,
+                                         const XDigits<CPL> &x, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks)
+            acc = fmaf(half_bits_to_float(scales[b]) * x.sc[j],
+                       dot_block_digits<QT>(row, b, x.d[j]), acc);
+    }
+    return wave_total(acc);
+}
+
+// As row_dot, reading the digits from LDS (rows swept once per wave).
+template <int QT, int CPL>
+__device__ __forceinline__ float row_dot_lds(const uint8_t *row,
+                                             const uint16_t *scales,
+                                             const uint32_t *xl,
+                                             const float *xsc, int blocks)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int b = lane + kWave * j;
+        if (b < blocks) {
+            uint4 d[6];
+            load_digits(xl, b, d);
+            acc = fmaf(half_bits_to_float(scales[b]) * xsc[b],
+                       dot_block_digits<QT>(row, b, d), acc);
         }
     }
     return wave_total(acc);
@@ -474,9 +615,9 @@ __device__ __forceinline__ void wg_share(int units, int &begin, int &end)
 template <class G> struct Lds {
     static constexpr int XN = cmax(G::FFN, G::DIM);
     static constexpr int H = 0;                      // raw h [DIM]
-    static constexpr int X = H + G::DIM;             // swizzled x
-    static constexpr int XSUM = X + XN;              // block sums
-    static constexpr int QKV = XSUM + XN / 32;       // q, k, v staging
+    static constexpr int X = H + G::DIM;             // swizzled x, then its digits
+    static constexpr int XSC = X + XN; // per block: digit scale, or sum (ffn)
+    static constexpr int QKV = XSC + XN / 32;        // q, k, v staging
     static constexpr int SCORES = QKV + G::DIM + 2 * G::KVD;
     static constexpr int R1 = cdiv(SCORES + kWaves * G::HPW * G::NP, 4) * 4;
     static constexpr int R2 = R1 + G::R1 / 4;
@@ -496,7 +637,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     extern __shared__ float4 lds4[];
     float *lds = reinterpret_cast<float *>(lds4);
     using L = Lds<G>;
-    float *h_raw = lds + L::H, *xs = lds + L::X, *xsum = lds + L::XSUM;
+    float *h_raw = lds + L::H, *xs = lds + L::X, *xsc = lds + L::XSC;
+    uint32_t *xl = reinterpret_cast<uint32_t *>(xs); // x's digits (dim-sized phases)
     float *qkv = lds + L::QKV, *scores = lds + L::SCORES, *red = lds + L::RED;
     uint8_t *r1 = reinterpret_cast<uint8_t *>(lds + L::R1);
     uint8_t *r2 = reinterpret_cast<uint8_t *>(lds + L::R2);
@@ -748,8 +890,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 if (row < G::DIM + G::KVD)
                     rope_cs = a.rope[size_t(pos) * (G::HD / 2) + (local % G::HD) / 2];
             }
-            Slice<G::DIM> nw;
-            nw.load(norm(l, false));
+            // this thread's quartet of the norm weights (stage_x)
+            float4 nw4 = reinterpret_cast<const float4 *>(norm(l, false))[threadIdx.x];
             float sq;
             if (l == 0) {
                 Slice<G::DIM> e;
@@ -759,11 +901,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             } else {
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
             }
-            stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
+            stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 2 + 13 * l);
             {
-                XRegs<G::CPL_DIM> x;
-                load_x(x, xs, xsum, G::BLK_DIM);
+                XDigits<G::CPL_DIM> x;
+                load_x(x, xl, xsc, G::BLK_DIM);
                 for (int pair = wave; pair < qkv_e - qkv_b; pair += kWaves) {
                     const int row = 2 * (qkv_b + pair);
                     const uint8_t *d0, *d1;
@@ -893,19 +1035,17 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 }
                 const float inv = 1.0f / total;
                 const int e0 = head * G::HD + 4 * r;
-                xs[swz(e0)] = acc.x * inv;
-                xs[swz(e0 + 1)] = acc.y * inv;
-                xs[swz(e0 + 2)] = acc.z * inv;
-                xs[swz(e0 + 3)] = acc.w * inv;
+                quartet_digits<G::QT>(make_float4(acc.x * inv, acc.y * inv, acc.z * inv,
+                                                  acc.w * inv),
+                                      e0 >> 5, (e0 >> 2) & 7, xl, xsc);
             }
             __syncthreads();
-            block_sums(xs, xsum, G::DIM);
             mark(it, 6 + 13 * l);
             for (int r = wave; r < wo_e - wo_b; r += kWaves) {
                 const uint8_t *d;
                 const uint16_t *s;
                 slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
-                const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xs, xsum, G::BLK_DIM);
+                const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xl, xsc, G::BLK_DIM);
                 if (lane == 0)
                     put(a.x_hidden + wo_b + r, h_raw[wo_b + r] + y, tag);
             }
@@ -918,13 +1058,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 8 + 13 * l);
 
             // ------------------------------------------ phase C: gate/up --
-            nw.load(norm(l, true));
+            nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
             sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
-            stage_x(h_raw, nw, rms_scale(wg_sum(sq, red), G::DIM), xs, xsum);
+            stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 9 + 13 * l);
             {
-                XRegs<G::CPL_DIM> x;
-                load_x(x, xs, xsum, G::BLK_DIM);
+                XDigits<G::CPL_DIM> x;
+                load_x(x, xl, xsc, G::BLK_DIM);
                 for (int pair = wave; pair < gu_e - gu_b; pair += kWaves) {
                     const uint8_t *dg, *du;
                     const uint16_t *sg, *su;
@@ -944,7 +1084,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // --------------------------------------------- phase D: down --
             take<G::FFN, true>(a.x_act, xs, tag - 1, error);
-            block_sums(xs, xsum, G::FFN);
+            block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {
                 const bool last = l + 1 == a.layer_count;
@@ -952,7 +1092,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const uint8_t *d;
                     const uint16_t *s;
                     slot(G::ROWS_DN, G::RB_FFN, G::SB_FFN, r, d, s, r1);
-                    const float y = row_dot_lds<G::QT, G::CPL_FFN>(d, s, xs, xsum, G::BLK_FFN);
+                    const float y = row_dot_floats<G::QT, G::CPL_FFN>(d, s, xs, xsc, G::BLK_FFN);
                     if (lane == 0) {
                         const float v = h_raw[dn_b + r] + y;
                         put(a.x_hidden + dn_b + r, v, tag);
