@@ -1,0 +1,78 @@
+"""Per-phase timeline of the cooperative token kernel.
+
+    python3 -m nutllm_amd.phase_timeline [workload]
+
+Runs one greedy generate of the workload (default ``tinyllama_int4``) to
+warm up, then a second one with every workgroup stamping the 100 MHz
+real-time clock at 13 marks per layer (``record_timeline(2)``), and prints
+medians over workgroups, layers and the steady iterations (the first two
+and the last are left out):
+
+- each compute segment of a layer (A: rmsnorm + Q/K/V rows + RoPE; B:
+  attention, then the Wo rows; C: rmsnorm + gate/up rows; D: W2 rows), and
+  the weight-DMA issue after each publish;
+- each exchange: from the last workgroup's publish to the median
+  workgroup holding the input (``ready``), and the publish skew (last
+  publish minus median publish).
+
+Mark k of layer l is column 2 + 13 l + k of ``timeline()``: 0 A input
+ready, 1 A published, 2 DMA issued, 3 B input ready, 4 attention done,
+5 B published, 6 DMA issued, 7 C input ready, 8 C published, 9 DMA
+issued, 10 D input ready, 11 D published, 12 next DMA issued.
+"""
+import sys
+
+import numpy as np
+
+from . import workloads
+
+MARKS = 13
+SEGMENTS = [("A rows", 0, 1), ("A dma issue", 1, 2), ("B attention", 3, 4),
+            ("B Wo rows", 4, 5), ("B dma issue", 5, 6), ("C rows", 7, 8),
+            ("C dma issue", 8, 9), ("D rows", 10, 11), ("D dma issue", 11, 12)]
+# (name, publish mark, ready mark, the ready mark's layer offset)
+EXCHANGES = [("q/k/v", 1, 3, 0), ("h after Wo", 5, 7, 0), ("act", 8, 10, 0),
+             ("h after W2", 11, 0, 1)]
+
+
+def summarise(t, layers):
+    """t: [workgroups, iterations, 2 + 13 layers] in microseconds."""
+    its = range(2, t.shape[1] - 1)
+    col = lambda l, k: 2 + MARKS * l + k
+    out = {}
+    for name, a, b in SEGMENTS:
+        d = [t[:, it, col(l, b)] - t[:, it, col(l, a)] for it in its for l in range(layers)]
+        out[name] = float(np.median(np.concatenate(d)))
+    for name, p, r, shift in EXCHANGES:
+        ready, skew = [], []
+        for it in its:
+            for l in range(layers - shift):
+                pub = t[:, it, col(l, p)]
+                ready.append(np.median(t[:, it, col(l + shift, r)]) - pub.max())
+                skew.append(pub.max() - np.median(pub))
+        out["exchange " + name] = float(np.mean(ready))
+        out["skew " + name] = float(np.mean(skew))
+    lay = [np.median(t[:, it, col(l + 1, 0)] - t[:, it, col(l, 0)])
+           for it in its for l in range(layers - 1)]
+    out["layer"] = float(np.median(lay))
+    out["classifier + argmax"] = float(np.median([np.median(t[:, it, 2] - t[:, it, 0])
+                                                  for it in its]))
+    return out
+
+
+def main(argv):
+    name = argv[1] if len(argv) > 1 else "tinyllama_int4"
+    model, prompt, gen = workloads.build_run(name)
+    dev = model.to_device()
+    dev.generate(prompt, gen)
+    dev.record_timeline(2)
+    ids, _ = dev.generate(prompt, gen)
+    n = len(ids)
+    t = dev.timeline(n)
+    print(f"{name}: {n} tokens, {dev.last_decode_ms() * 1e3 / n:.1f} us per token (HIP events)")
+    for key, v in summarise(t, model.config.layers).items():
+        print(f"  {key:24s} {v:6.2f} us")
+
+
+if __name__ == "__main__":
+    main(sys.argv)
