@@ -240,6 +240,34 @@ def test_tinyllama_int4_paths_greedy(gpu, tinyllama_int4, path):
     dev.set_path(0)
 
 
+@pytest.mark.parametrize("scale", [300.0, 1e-30], ids=["outliers", "tiny_dims"])
+def test_token_kernel_wide_range_activations(gpu, scale):
+    """Every 257th embedding dimension scaled by 300 (outlier features, as in
+    trained models) or by 1e-30 (elements far below their block's maximum):
+    the token kernel's integer digit dots, which keep x to 2^-23.7 of each
+    32-block's maximum, still hold the fp32 bar on the post-prompt and
+    next-token hidden states and on the new K/V rows."""
+    O.orc().orc_set_threads(16)
+    model, prompt, _ = W.build_run("tinyllama_int4")
+    model.embeddings[:, ::257] *= np.float32(scale)
+    dev = model.to_device()
+    dev.set_path(2)
+    om = O.oracle_model(model)
+    cache = gpu.KVCache(model.config)
+    h = dev.prefill(cache, prompt)
+    assert rel_l2(h, om.prefill(prompt)) <= TOL
+    token = int(prompt[0])
+    h2 = dev.decode(cache, token)
+    assert rel_l2(h2, om.decode(token)) <= TOL
+    pos = len(prompt)
+    for layer in (0, model.config.layers - 1):
+        for head in range(model.config.kv_heads):
+            k, v = cache.key_value(layer, head, pos)
+            rk, rv = om.kv_row(layer, head, pos)
+            assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+    dev.close()
+
+
 def test_token_kernel_rejects_unsupported_shape(gpu, tiny):
     model, prompt, _, dev = tiny
     dev.set_path(2)
