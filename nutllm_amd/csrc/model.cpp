@@ -486,7 +486,7 @@ namespace {
 
 // The cooperative token kernel runs when the model shape has an
 // instantiation, the device can hold its grid, and every position of the
-// launch fits the fused attention pass.
+// launch fits the fused attention pass or, beyond it, the split one.
 bool use_token_kernel(nut_model &m, size_t end_length)
 {
     if (m.path == 1)
@@ -495,7 +495,7 @@ bool use_token_kernel(nut_model &m, size_t end_length)
     for (const DeviceLayer &l : m.layers)
         arena = arena && l.in_arena;
     const bool ok = arena && token_kernel_supported(m.type, m.shape) &&
-                    end_length <= size_t(token_kernel_max_positions(m.type, m.shape));
+                    end_length <= size_t(token_kernel_long_positions(m.type, m.shape));
     if (m.path == 2 && !ok)
         fail(NUT_EINVAL, "token kernel: shape or context not supported");
     return ok;
@@ -532,6 +532,11 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.x_hidden = x + s.dim + 2 * kvd;
     a.x_act = a.x_hidden + s.dim;
     a.x_part = a.x_act + s.ffn_dim;
+    a.x_apart = a.x_part + 2 * kTokenGrid;
+    a.x_ctx = a.x_apart + size_t(kTokenGrid) * (s.heads / s.kv_heads) * (s.head_dim + 2);
+    // beyond the fused attention pass, attention is split over the grid
+    a.long_attention =
+        start + n_iter > size_t(token_kernel_max_positions(m.type, s)) ? 1 : 0;
     a.hidden_in = hidden_in;
     a.hidden_out = hidden_out;
     a.tokens_in = tokens_in;

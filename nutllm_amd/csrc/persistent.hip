@@ -70,6 +70,15 @@ struct Geo {
     // count) and the QKV, gate/up and W2 rows of a phase
     static constexpr int R1 = cmax(cmax(KV_BYTES, W_QKV), cmax(W_GU, W_DN));
     static constexpr int R2 = W_WO;
+    // Split attention for long contexts: workgroup b takes KV head
+    // b / SPLITS and the b % SPLITS-th run of at most PMAX positions.
+    static constexpr int SPLITS = kGrid / KVH;
+    static constexpr int PMAX = 64;
+    static_assert(SPLITS == kWave, "one merge lane per split");
+    static_assert(2 * PMAX * KROW * 4 <= R1 && GROUP * PMAX <= kWaves * HPW * NP,
+                  "split attention staging");
+    static_assert(GROUP == 2 * HPW && kGrid == HEADS * (HD / 8),
+                  "split attention: two waves per KV head, eight context values per merger");
     // weight arena layout of one layer
     static constexpr LayerLayout LAY = layer_layout(QT, DIM, FFN, KVD);
     static_assert(DIM % 32 == 0 && FFN % 32 == 0, "block-aligned rows");
@@ -610,6 +619,137 @@ __device__ __forceinline__ void wg_share(int units, int &begin, int &end)
     end = int((long long)units * (blockIdx.x + 1) / kGrid);
 }
 
+// ------------------------------------------------- split attention --
+
+// dst[i] = value of *addr(i) once tagged, i < N; as take (batched
+// re-polls, bounded), for words scattered over an exchange buffer. Ends
+// with a barrier.
+template <int N, class Addr>
+__device__ void take_words(Addr addr, float *dst, unsigned tag, int *error)
+{
+    constexpr int PER = cdiv(N, kThreads);
+    uint64_t v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        v[u] = i < N ? load_coherent(addr(i)) : uint64_t(tag) << 32;
+    }
+    for (int spins = 0;; spins++) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            stale |= unsigned(v[u] >> 32) != tag;
+        if (!stale)
+            break;
+        if ((spins & 63) == 63 && failed(error))
+            break;
+        if (spins > kSpinLimit) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            if (unsigned(v[u] >> 32) != tag)
+                v[u] = load_coherent(addr(threadIdx.x + u * kThreads));
+    }
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < N)
+            dst[i] = __uint_as_float(unsigned(v[u]));
+    }
+    __syncthreads();
+}
+
+// Attention of a long context split over the grid (src/quant_model.cpp:
+// 45-108 computes the same softmax over all positions at once). Workgroup
+// b owns KV head ag = b / SPLITS and its cnt positions [ap0, ap1) (K and V
+// rows staged at kst / vst): wave w computes, for query head w of the KV
+// head's group, the run's maximum score m, l = sum exp(s_p - m) and
+// o = sum exp(s_p - m) V_p, published with `tag` as x_apart words
+// [b][head][o 0..HD-1, m, l]. Then workgroup b merges context values
+// 8 (b % 8) .. +7 of head b / 8 over its KV head's SPLITS runs (lane sp of
+// wave 0 takes run sp): M = max m, context = sum e^(m - M) o / sum
+// e^(m - M) l, published with tag + 1 into x_ctx. mb: LDS, SPLITS * 10
+// floats.
+template <class G>
+__device__ void split_attention(int cnt, int ag, const float *kst, const float *vst,
+                                const float *qkv, float *scores, float *mb,
+                                const TokenArgs &a, unsigned tag, int *error)
+{
+    static_assert(G::GROUP == kWaves && G::PMAX == kWave && G::HD == kWave,
+                  "split attention: a wave per query head, a lane per position and per dim");
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    {
+        // wave w: query head w of the group; lane p: position p's score,
+        // then lane d: context dim d
+        const float4 *q4 =
+            reinterpret_cast<const float4 *>(qkv + (ag * G::GROUP + wave) * G::HD);
+        float sv = -INFINITY;
+        if (lane < cnt) {
+            const float4 *k4 = reinterpret_cast<const float4 *>(kst + lane * G::KROW);
+            float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int d4 = 0; d4 < 16; d4 += 2) {
+                const float4 k0 = k4[d4], q0 = q4[d4];
+                const float4 k1 = k4[d4 + 1], q1 = q4[d4 + 1];
+                a0 = fmaf(q0.x, k0.x, a0);
+                a1 = fmaf(q1.x, k1.x, a1);
+                a0 = fmaf(q0.y, k0.y, a0);
+                a1 = fmaf(q1.y, k1.y, a1);
+                a0 = fmaf(q0.z, k0.z, a0);
+                a1 = fmaf(q1.z, k1.z, a1);
+                a0 = fmaf(q0.w, k0.w, a0);
+                a1 = fmaf(q1.w, k1.w, a1);
+            }
+            sv = (a0 + a1) * a.attn_scale;
+        }
+        const float m = wave_maximum(sv);
+        const float e = lane < cnt ? expf(sv - m) : 0.0f;
+        const float total = wave_total(e);
+        float *sc = scores + wave * G::PMAX;
+        sc[lane] = e;
+        // the wave's weights, written by every lane, before any lane reads
+        // them (LDS runs one wave's accesses in order; the fences keep the
+        // compiler's order)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float o = 0.0f;
+#pragma unroll 8
+        for (int p = 0; p < cnt; p++)
+            o = fmaf(sc[p], vst[p * G::KROW + lane], o);
+        uint64_t *dst = a.x_apart + size_t(blockIdx.x * G::GROUP + wave) * (G::HD + 2);
+        put(dst + lane, o, tag);
+        if (lane == 0) {
+            put(dst + G::HD, m, tag);
+            put(dst + G::HD + 1, total, tag);
+        }
+    }
+    const int mh = blockIdx.x >> 3, md0 = (blockIdx.x & 7) * 8;
+    const int mg = mh / G::GROUP, mhl = mh % G::GROUP;
+    take_words<G::SPLITS * 10>(
+        [&](int i) {
+            const int sp = i / 10, j = i - sp * 10;
+            return a.x_apart + size_t((mg * G::SPLITS + sp) * G::GROUP + mhl) * (G::HD + 2) +
+                   (j < 8 ? md0 + j : G::HD + j - 8);
+        },
+        mb, tag, error);
+    if (wave == 0) {
+        const float pm = mb[lane * 10 + 8], pl = mb[lane * 10 + 9];
+        const float mx = wave_maximum(pm);
+        const float w = pm == -INFINITY ? 0.0f : expf(pm - mx);
+        const float total = wave_total(w * pl);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float c = wave_total(w * mb[lane * 10 + j]);
+            if (lane == 0)
+                put(a.x_ctx + mh * G::HD + md0 + j, c / total, tag + 1);
+        }
+    }
+}
+
 // ------------------------------------------------------------- kernel --
 
 template <class G> struct Lds {
@@ -631,7 +771,7 @@ template <class G> struct Lds {
 // CLASSIFY: the generate loop (classifier + argmax first in every
 // iteration); otherwise the prefill loop over a.tokens_in. Two kernels, so
 // profiles tell the launches apart.
-template <class G, bool CLASSIFY>
+template <class G, bool CLASSIFY, bool LONG>
 __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 {
     extern __shared__ float4 lds4[];
@@ -943,14 +1083,28 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             __syncthreads();
             mark(it, 3 + 13 * l);
             const int n = pos + 1;
-            float *vst = kst + G::KVH * n * G::KROW;
-            if (pos > 0)
+            // LONG: this workgroup's attention unit is KV head ag over
+            // positions [ap0, ap1), K rows at kst and V rows at vst
+            const int ag = blockIdx.x / G::SPLITS;
+            const int per = cdiv(n, G::SPLITS);
+            const int ap0 = min(n, int(blockIdx.x % G::SPLITS) * per);
+            const int ap1 = min(n, ap0 + per);
+            float *vst = LONG ? kst + G::PMAX * G::KROW : kst + G::KVH * n * G::KROW;
+            if (LONG) {
+                const int hist = max(0, min(ap1, pos) - ap0); // rows already cached
+                if (hist > 0) {
+                    const size_t row0 = size_t(ag) * a.max_seq + ap0;
+                    dma_padded_rows(kst, kc + row0 * G::HD, hist);
+                    dma_padded_rows(vst, vc + row0 * G::HD, hist);
+                }
+            } else if (pos > 0) {
                 for (int kvh = 0; kvh < G::KVH; kvh++) {
                     dma_padded_rows(kst + kvh * n * G::KROW,
                                     kc + size_t(kvh) * a.max_seq * G::HD, pos);
                     dma_padded_rows(vst + kvh * n * G::KROW,
                                     vc + size_t(kvh) * a.max_seq * G::HD, pos);
                 }
+            }
             stage_wo(l);
             mark(it, 4 + 13 * l);
 
@@ -958,16 +1112,33 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
             take<G::DIM + 2 * G::KVD, false>(a.x_qkv, qkv, tag - 1, error);
-            for (int i = threadIdx.x; i < 2 * G::KVD; i += kThreads) {
-                const int which = i >= G::KVD;
-                const int j = i - which * G::KVD;
-                const int kvh = j / G::HD, d = j - kvh * G::HD;
-                (which ? vst : kst)[(kvh * n + pos) * G::KROW + d] = qkv[G::DIM + i];
+            if (LONG) {
+                // the new position's K/V row, when it falls in this unit
+                if (pos >= ap0 && pos < ap1)
+                    for (int i = threadIdx.x; i < 2 * G::HD; i += kThreads) {
+                        const int which = i >= G::HD, d = i - which * G::HD;
+                        (which ? vst : kst)[(pos - ap0) * G::KROW + d] =
+                            qkv[G::DIM + which * G::KVD + ag * G::HD + d];
+                    }
+            } else {
+                for (int i = threadIdx.x; i < 2 * G::KVD; i += kThreads) {
+                    const int which = i >= G::KVD;
+                    const int j = i - which * G::KVD;
+                    const int kvh = j / G::HD, d = j - kvh * G::HD;
+                    (which ? vst : kst)[(kvh * n + pos) * G::KROW + d] = qkv[G::DIM + i];
+                }
             }
 
             __syncthreads();
             mark(it, 5 + 13 * l);
-            {
+            if constexpr (LONG) {
+                split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, tag, error);
+                tag += 2;
+                // the whole context, as digits for the Wo rows
+                take<G::DIM, false>(a.x_ctx, qkv, tag - 1, error);
+                quartet_digits<G::QT>(reinterpret_cast<const float4 *>(qkv)[threadIdx.x],
+                                      threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
+            } else {
                 // Wave w: query heads 4w..4w+3, all of kv head 4w / GROUP.
                 // Lane (hh = lane / 16, r = lane % 16): scores of head hh at
                 // positions r, r + 16, ...; then context quad r of head hh.
@@ -1148,10 +1319,10 @@ int device_cus()
     return cus;
 }
 
-template <class G, bool CLASSIFY>
+template <class G, bool CLASSIFY, bool LONG>
 void launch_as(const TokenArgs &args, hipStream_t stream)
 {
-    const auto kernel = token_kernel<G, CLASSIFY>;
+    const auto kernel = token_kernel<G, CLASSIFY, LONG>;
     hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
                                   int(Lds<G>::BYTES)),
@@ -1163,8 +1334,10 @@ void launch_as(const TokenArgs &args, hipStream_t stream)
               "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     require(per_cu >= 1 && device_cus() >= kGrid, NUT_EDEVICE,
             "token kernel: grid does not fit the device");
-    require(args.start_len + args.n_iter <= G::NP, NUT_EINVAL,
-            "token kernel: context exceeds the fused attention pass");
+    require(args.start_len + args.n_iter <= (LONG ? G::SPLITS * G::PMAX : G::NP), NUT_EINVAL,
+            "token kernel: context exceeds the attention pass");
+    require(!LONG || (args.x_apart != nullptr && args.x_ctx != nullptr), NUT_EINVAL,
+            "token kernel: split attention needs its exchange buffers");
     TokenArgs a = args;
     void *params[] = {&a};
     hip_check(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kernel),
@@ -1176,10 +1349,17 @@ void launch_as(const TokenArgs &args, hipStream_t stream)
 template <class G>
 void launch(const TokenArgs &args, hipStream_t stream)
 {
-    if (args.classify)
-        launch_as<G, true>(args, stream);
-    else
-        launch_as<G, false>(args, stream);
+    if (args.long_attention) {
+        if (args.classify)
+            launch_as<G, true, true>(args, stream);
+        else
+            launch_as<G, false, true>(args, stream);
+    } else {
+        if (args.classify)
+            launch_as<G, true, false>(args, stream);
+        else
+            launch_as<G, false, false>(args, stream);
+    }
 }
 
 } // namespace
@@ -1200,10 +1380,22 @@ int token_kernel_max_positions(int type, const DecodeShape &s)
     return 0;
 }
 
+int token_kernel_long_positions(int type, const DecodeShape &s)
+{
+    if (shape_is<TinyLlamaInt4>(s, type))
+        return TinyLlamaInt4::SPLITS * TinyLlamaInt4::PMAX;
+    if (shape_is<TinyLlamaInt8>(s, type))
+        return TinyLlamaInt8::SPLITS * TinyLlamaInt8::PMAX;
+    return 0;
+}
+
 size_t token_exchange_entries(const DecodeShape &s)
 {
     const size_t kvd = size_t(s.kv_heads) * s.head_dim;
-    return (s.dim + 2 * kvd) + s.dim + s.ffn_dim + 2 * kGrid;
+    const size_t group = s.heads / (s.kv_heads == 0 ? s.heads : s.kv_heads);
+    // q/k/v, h, act, classifier partials; split attention partials, context
+    return (s.dim + 2 * kvd) + s.dim + s.ffn_dim + 2 * kGrid +
+           size_t(kGrid) * group * (s.head_dim + 2) + s.dim;
 }
 
 void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,

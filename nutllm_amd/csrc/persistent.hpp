@@ -23,6 +23,11 @@ struct TokenArgs {
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
     uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
+    // Long contexts (long_attention != 0): attention is split over the
+    // workgroups; x_apart holds each workgroup's partial (m, l, o) for the
+    // query heads of its KV head, x_ctx the merged context.
+    uint64_t *x_apart, *x_ctx;
+    int long_attention;
     const float *hidden_in;   // hidden state before iteration 0 (classify)
     float *hidden_out;        // hidden state after the last decode step
     const int *tokens_in;     // per-iteration tokens (prefill)
@@ -52,6 +57,9 @@ __host__ __device__ inline int marks_per_iteration(int layers)
 // Longest context (positions) the kernel's fused attention phase handles
 // for this shape; 0 when the shape has no instantiation.
 int token_kernel_max_positions(int type, const DecodeShape &s);
+// Longest context of the split-attention variant (long_attention), used
+// beyond token_kernel_max_positions; 0 when the shape has no instantiation.
+int token_kernel_long_positions(int type, const DecodeShape &s);
 
 // True when the cooperative kernel has an instantiation for this shape and
 // quant type and the device can hold its grid.

@@ -268,6 +268,52 @@ def test_token_kernel_wide_range_activations(gpu, scale):
     dev.close()
 
 
+@pytest.mark.parametrize("qtype", [0, 1], ids=["int8", "int4"])
+def test_token_kernel_split_attention(gpu, qtype):
+    """Contexts beyond the token kernel's fused attention pass (48 positions
+    INT4, 44 INT8): attention is split over the grid (each workgroup one KV
+    head over a run of positions, each context value merged over the runs
+    by one workgroup). From a 300-token prefill on the step kernels, each
+    token-kernel decode step's hidden state and new K/V rows within rel-L2
+    1e-5 of the oracle; then generate() (batched prefill, split-attention
+    decode loop) gives the oracle's greedy ids."""
+    O.orc().orc_set_threads(16)
+    model = W.build("tinyllama", qtype, 3, 512)
+    c = model.config
+    prompt = gpu.synth_tokens(23, c.vocab_size, 300)
+    dev = model.to_device()
+    om = O.oracle_model(model)
+    try:
+        dev.set_path(1)
+        cache = gpu.KVCache(c)
+        hd = dev.prefill(cache, prompt)
+        ho = om.prefill(prompt)
+        assert rel_l2(hd, ho) <= TOL
+        dev.set_path(2)
+        ref = []
+        for step in range(6):
+            token = int(np.argmax(om.logits(ho)))
+            if token == c.eos_token:
+                break
+            ref.append(token)
+            ho, hd = om.decode(token), dev.decode(cache, token)
+            err = rel_l2(hd, ho)
+            print(f"qtype {qtype} step {step}: hidden rel-L2 {err:.2e}", flush=True)
+            assert err <= TOL
+            pos = len(prompt) + step
+            for layer in (0, c.layers - 1):
+                for kvh in range(c.kv_heads):
+                    k, v = cache.key_value(layer, kvh, pos)
+                    rk, rv = om.kv_row(layer, kvh, pos)
+                    assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+        dev.set_path(0)
+        ids, _ = dev.generate(prompt, len(ref))
+        assert ids == ref
+    finally:
+        dev.set_path(0)
+        dev.close()
+
+
 def test_token_kernel_rejects_unsupported_shape(gpu, tiny):
     model, prompt, _, dev = tiny
     dev.set_path(2)
