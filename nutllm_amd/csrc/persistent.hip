@@ -669,8 +669,8 @@ __device__ void take_words(Addr addr, float *dst, unsigned tag, int *error)
 // head's group, the run's maximum score m, l = sum exp(s_p - m) and
 // o = sum exp(s_p - m) V_p, published with `tag` as x_apart words
 // [b][head][o 0..HD-1, m, l]. Then workgroup b merges context values
-// 8 (b % 8) .. +7 of head b / 8 over its KV head's SPLITS runs (lane sp of
-// wave 0 takes run sp): M = max m, context = sum e^(m - M) o / sum
+// 8 (b % 8) .. +7 of head b / 8 over its KV head's SPLITS runs (wave w
+// value w, lane sp run sp): M = max m, context = sum e^(m - M) o / sum
 // e^(m - M) l, published with tag + 1 into x_ctx. mb: LDS, SPLITS * 10
 // floats.
 template <class G>
@@ -736,17 +736,15 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
                    (j < 8 ? md0 + j : G::HD + j - 8);
         },
         mb, tag, error);
-    if (wave == 0) {
+    {
+        // wave w merges context value md0 + w
         const float pm = mb[lane * 10 + 8], pl = mb[lane * 10 + 9];
         const float mx = wave_maximum(pm);
         const float w = pm == -INFINITY ? 0.0f : expf(pm - mx);
         const float total = wave_total(w * pl);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float c = wave_total(w * mb[lane * 10 + j]);
-            if (lane == 0)
-                put(a.x_ctx + mh * G::HD + md0 + j, c / total, tag + 1);
-        }
+        const float c = wave_total(w * mb[lane * 10 + wave]);
+        if (lane == 0)
+            put(a.x_ctx + mh * G::HD + md0 + wave, c / total, tag + 1);
     }
 }
 
