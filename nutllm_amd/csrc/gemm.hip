@@ -2,8 +2,8 @@
 // src/threading.cpp:163-181).
 //
 // v_mfma_f32_16x16x4f32 keeps fp32 inputs and accumulation. A workgroup of
-// four waves owns a 64x64 tile of C; each wave a 32x32 quarter (2x2 MFMA
-// tiles).
+// four waves owns a 64x64 tile of C (32x32 when 64x64 tiles would not give
+// every CU one); each wave a quarter (2x2 or 1x1 MFMA tiles).
 //   tiled    M, N, K multiples of 64, 16-byte aligned rows: K advances 64
 //            at a time; the next slice is loaded (float4) into registers
 //            while the MFMAs run on the current one in LDS; A is stored
@@ -94,84 +94,108 @@ __global__ __launch_bounds__(kThreads) void matmul_f32_kernel(
 
 constexpr int TK = 64;
 
+// The tiled kernel for a TBM x TBN tile of C (64 x 64, or 32 x 32 when the
+// 64 x 64 grid would leave CUs idle): waves in a 2 x 2 grid, each a
+// (TBM / 2) x (TBN / 2) block of 16 x 16 MFMA tiles. The next D k-slices
+// are in flight in registers while one is multiplied from LDS (a slice's
+// MFMAs take far less than a load's latency for the small tile).
+template <int TBM, int TBN, int D>
 __global__ __launch_bounds__(kThreads) void matmul_f32_tiled(
     const float *__restrict__ a, const float *__restrict__ b,
     float *__restrict__ c, int m, int k, int n)
 {
-    __shared__ float at[TK][BM + 4]; // A slice, transposed: at[k][row]
-    __shared__ float bs[TK][BN + 4];
+    constexpr int TI = TBM / 32, TJ = TBN / 32; // MFMA tiles per wave
+    constexpr int AH = TBM * TK / 4 / kThreads; // A float4 per thread
+    constexpr int BH = TK * TBN / 4 / kThreads; // B float4 per thread
+    static_assert(TI >= 1 && TJ >= 1 && AH >= 1 && BH >= 1, "tile shape");
+    __shared__ float at[TK][TBM + 4]; // A slice, transposed: at[k][row]
+    __shared__ float bs[TK][TBN + 4];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
-    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
-    // loader mapping: A slice 64x64 = 1024 float4, B slice 64x64 = 1024
-    // float4; four of each per thread
-    const int ar = tid >> 4, ac = (tid & 15) * 4;  // A: rows ar + 16 h
-    const int br = tid >> 4, bc = (tid & 15) * 4;  // B: rows br + 16 h
+    const int row0 = blockIdx.y * TBM, col0 = blockIdx.x * TBN;
+    const int wr = (wave >> 1) * (TBM / 2), wc = (wave & 1) * (TBN / 2);
+    // loader mapping: A slice TBM x 64 (16 float4 per row), B slice
+    // 64 x TBN (TBN / 4 float4 per row)
+    const int ar = tid >> 4, ac = (tid & 15) * 4;   // A: rows ar + 16 h
+    constexpr int BQ = TBN / 4;                      // float4 per B row
+    const int br = tid / BQ, bc = (tid % BQ) * 4;   // B: rows br + (kThreads / BQ) h
+    constexpr int BRS = kThreads / BQ;
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
     const float4 *b4 = reinterpret_cast<const float4 *>(b);
     const size_t lda4 = size_t(k) / 4, ldb4 = size_t(n) / 4;
-    auto load = [&](int k0, float4 (&ra)[4], float4 (&rb)[4]) {
+    auto load = [&](int k0, float4 (&ra)[AH], float4 (&rb)[BH]) {
 #pragma unroll
-        for (int h = 0; h < 4; h++) {
+        for (int h = 0; h < AH; h++)
             ra[h] = a4[size_t(row0 + ar + 16 * h) * lda4 + (k0 + ac) / 4];
-            rb[h] = b4[size_t(k0 + br + 16 * h) * ldb4 + (col0 + bc) / 4];
-        }
-    };
-    auto store = [&](const float4 (&ra)[4], const float4 (&rb)[4]) {
 #pragma unroll
-        for (int h = 0; h < 4; h++) {
+        for (int h = 0; h < BH; h++)
+            rb[h] = b4[size_t(k0 + br + BRS * h) * ldb4 + (col0 + bc) / 4];
+    };
+    auto store = [&](const float4 (&ra)[AH], const float4 (&rb)[BH]) {
+#pragma unroll
+        for (int h = 0; h < AH; h++) {
             const int r = ar + 16 * h;
             at[ac][r] = ra[h].x;
             at[ac + 1][r] = ra[h].y;
             at[ac + 2][r] = ra[h].z;
             at[ac + 3][r] = ra[h].w;
-            *reinterpret_cast<float4 *>(&bs[br + 16 * h][bc]) = rb[h];
         }
+#pragma unroll
+        for (int h = 0; h < BH; h++)
+            *reinterpret_cast<float4 *>(&bs[br + BRS * h][bc]) = rb[h];
     };
-    floatx4 acc[2][2];
+    floatx4 acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < TJ; j++)
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    float4 ra[4], rb[4];
-    load(0, ra, rb);
-    for (int k0 = 0; k0 < k; k0 += TK) {
-        store(ra, rb);
+    float4 ra[D][AH], rb[D][BH];
+#pragma unroll
+    for (int j = 0; j < D; j++)
+        if (j * TK < k)
+            load(j * TK, ra[j], rb[j]);
+    auto slice = [&](int k0, float4 (&sa)[AH], float4 (&sb)[BH]) {
+        store(sa, sb);
         __syncthreads();
-        if (k0 + TK < k)
-            load(k0 + TK, ra, rb); // in flight during the MFMAs below
-        // fragments of four k-steps are read together, then 16 MFMAs
+        if (k0 + D * TK < k)
+            load(k0 + D * TK, sa, sb); // in flight during the MFMAs below
+        // fragments of four k-steps are read together, then the MFMAs
         // issue back to back
 #pragma unroll
         for (int kq = 0; kq < TK; kq += 16) {
-            float af[4][2], bf[4][2];
+            float af[4][TI], bf[4][TJ];
 #pragma unroll
             for (int s4 = 0; s4 < 4; s4++) {
                 const int ka = kq + 4 * s4 + (lane >> 4);
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < TI; i++)
                     af[s4][i] = at[ka][wr + i * 16 + (lane & 15)];
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < TJ; j++)
                     bf[s4][j] = bs[ka][wc + j * 16 + (lane & 15)];
             }
 #pragma unroll
             for (int s4 = 0; s4 < 4; s4++)
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < TI; i++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < TJ; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                             af[s4][i], bf[s4][j], acc[i][j], 0, 0, 0);
         }
         __syncthreads();
+    };
+    for (int k0 = 0; k0 < k; k0 += D * TK) {
+#pragma unroll
+        for (int j = 0; j < D; j++)
+            if (k0 + j * TK < k) // workgroup-uniform
+                slice(k0 + j * TK, ra[j], rb[j]);
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < TJ; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int r = row0 + wr + i * 16 + 4 * (lane >> 4) + v;
@@ -188,12 +212,18 @@ void launch_matmul_f32(const float *a, const float *b, float *c, int m, int k,
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
     const bool aligned = ((reinterpret_cast<uintptr_t>(a) |
                            reinterpret_cast<uintptr_t>(b)) & 15) == 0;
-    if (aligned && m % BM == 0 && n % BN == 0 && k % TK == 0)
-        hipLaunchKernelGGL(matmul_f32_tiled, grid, dim3(kThreads), 0, stream,
-                           a, b, c, m, k, n);
-    else
+    if (aligned && m % BM == 0 && n % BN == 0 && k % TK == 0) {
+        // 32 x 32 tiles when 64 x 64 ones would leave CUs without a tile
+        if (size_t(m / BM) * (n / BN) < 256)
+            hipLaunchKernelGGL((matmul_f32_tiled<32, 32, 1>), dim3(n / 32, m / 32),
+                               dim3(kThreads), 0, stream, a, b, c, m, k, n);
+        else
+            hipLaunchKernelGGL((matmul_f32_tiled<64, 64, 1>), grid, dim3(kThreads), 0, stream,
+                               a, b, c, m, k, n);
+    } else {
         hipLaunchKernelGGL(matmul_f32_kernel, grid, dim3(kThreads), 0, stream,
                            a, b, c, m, k, n);
+    }
     check_launch("threaded matmul");
 }
 
