@@ -206,9 +206,10 @@ int nut_generate_greedy(nut_model *m, const int *prompt, size_t prompt_len,
 /* Execution path of decode / prefill / generate (no reference counterpart;
  * every path computes the same function): NUT_PATH_AUTO picks the
  * cooperative token kernel when the shape has an instantiation and the
- * context fits its fused attention pass, else per-phase step kernels;
- * NUT_PATH_STEPS forces the step kernels; NUT_PATH_TOKEN forces the token
- * kernel and fails with NUT_EINVAL where it does not apply. */
+ * context fits its attention (fused up to 44-48 positions, split over the
+ * grid up to 4,096), else per-phase step kernels; NUT_PATH_STEPS forces the
+ * step kernels; NUT_PATH_TOKEN forces the token kernel and fails with
+ * NUT_EINVAL where it does not apply. */
 enum { NUT_PATH_AUTO = 0, NUT_PATH_STEPS = 1, NUT_PATH_TOKEN = 2 };
 int nut_model_set_path(nut_model *m, int path);
 
