@@ -1,6 +1,6 @@
 /* nut_oracle.c — CPU oracle for nutllm's quantised token loop.
  *
- * TEST INFRASTRUCTURE: the checker for the HIP path and the "port" CPU
+ * TEST INFRASTRUCTURE: the oracle for the HIP path and the "port" CPU
  * baseline. Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg load it; the product library never does.
  *

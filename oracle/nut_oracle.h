@@ -1,6 +1,6 @@
 /* nut_oracle.h — CPU oracle for nutllm's quantised token loop.
  *
- * TEST INFRASTRUCTURE. This is the checker, never the thing measured or
+ * TEST INFRASTRUCTURE. It checks the HIP path and is never the thing measured or
  * shipped: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it. The product path (nutllm_amd) never links or calls it.
  *
