@@ -314,6 +314,43 @@ def test_token_kernel_split_attention(gpu, qtype):
         dev.close()
 
 
+def test_token_kernel_split_attention_max_context(gpu):
+    """The split attention at its limit: max_seq 4096, the last decode step
+    at 4096 positions (64 per run, every run full). Two caches filled by the
+    same batched prefill of 4090 tokens (deterministic, so identical); the
+    token kernel on one and the step kernels (checked against the oracle up
+    to 1100 positions) on the other agree on each of six decode steps'
+    hidden state and new K/V rows within rel-L2 1e-5."""
+    model = W.build("tinyllama", 1, 3, 4096)
+    c = model.config
+    prompt = gpu.synth_tokens(29, c.vocab_size, 4090)
+    tokens = [int(t) for t in gpu.synth_tokens(31, c.vocab_size, 6)]
+    dev = model.to_device()
+    try:
+        dev.set_path(0)
+        cache_t, cache_s = gpu.KVCache(c), gpu.KVCache(c)
+        h_t = dev.prefill(cache_t, prompt)
+        h_s = dev.prefill(cache_s, prompt)
+        assert np.array_equal(h_t, h_s)
+        for step, token in enumerate(tokens):
+            dev.set_path(2)
+            h_t = dev.decode(cache_t, token)
+            dev.set_path(1)
+            h_s = dev.decode(cache_s, token)
+            err = rel_l2(h_t, h_s)
+            print(f"position {len(prompt) + step}: hidden rel-L2 {err:.2e}", flush=True)
+            assert err <= TOL
+            pos = len(prompt) + step
+            for layer in (0, c.layers - 1):
+                for kvh in range(c.kv_heads):
+                    kt, vt = cache_t.key_value(layer, kvh, pos)
+                    ks, vs = cache_s.key_value(layer, kvh, pos)
+                    assert rel_l2(kt, ks) <= TOL and rel_l2(vt, vs) <= TOL
+    finally:
+        dev.set_path(0)
+        dev.close()
+
+
 def test_token_kernel_rejects_unsupported_shape(gpu, tiny):
     model, prompt, _, dev = tiny
     dev.set_path(2)
