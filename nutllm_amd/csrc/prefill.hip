@@ -511,22 +511,25 @@ __global__ __launch_bounds__(kThreads) void kv_limbs_kernel(
 // layouts (checked on the device): A[i][k]: lane i % 16 + 16 g holds k =
 // 8 g .. 8 g + 7; B[k][n]: lane n % 16 + 16 g the same k; D[i][n]: lane
 // n + 16 (i / 4), element i % 4.
-template <int HD>
-__global__ __launch_bounds__(kThreads) void attention_prefill_f16(
+// HEADS query heads of one KV head per workgroup (4 waves each, 64 query
+// rows), sharing each K/V tile they stage.
+template <int HD, int HEADS>
+__global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     const float *q, const _Float16 *k_hi, const _Float16 *k_lo, const _Float16 *vt_hi,
     const _Float16 *vt_lo, _Float16 *ctx_hi, _Float16 *ctx_lo, int t_count, int t_pad,
     int heads, int kv_heads, float scale)
 {
+    constexpr int NT = 64 * 4 * HEADS;                     // threads
     constexpr int KP = HD + 8, VP = AK + 8, PP = AK + 8; // rows padded by 16 bytes
     constexpr int KB = HD / 32;                            // 32-wide k blocks of a head
     __shared__ __attribute__((aligned(16))) _Float16 ksh[AK][KP], ksl[AK][KP];
     __shared__ __attribute__((aligned(16))) _Float16 vsh[HD][VP], vsl[HD][VP];
-    __shared__ __attribute__((aligned(16))) _Float16 psh[4][16][PP], psl[4][16][PP];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __attribute__((aligned(16))) _Float16 psh[4 * HEADS][16][PP], psl[4 * HEADS][16][PP];
+    const int tid = threadIdx.x, lane = tid & 63, wave_all = tid >> 6, wave = wave_all & 3;
     const int li = lane & 15, lg = lane >> 4;
     // heads vary fastest and the longest query tiles (the most key tiles
     // under the causal mask) are dispatched first
-    const int head = blockIdx.x, g = head / (heads / kv_heads);
+    const int head = blockIdx.x * HEADS + (wave_all >> 2), g = head / (heads / kv_heads);
     const int t0 = (gridDim.y - 1 - blockIdx.y) * AQ;
     const int dim = heads * HD;
     // Q limbs of this wave's rows: A[i = li][k = 32 kb + 8 lg + j]
@@ -574,13 +577,13 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_f16(
     for (int p0 = 0; p0 <= last; p0 += AK) {
         __syncthreads(); // previous tile's readers are done
         // K tile rows p0 .. p0 + 63 (16-byte pieces), V^T tile [d][p0 ..]
-        for (int e = tid; e < AK * HD / 8; e += kThreads) {
+        for (int e = tid; e < AK * HD / 8; e += NT) {
             const int j = e / (HD / 8), c8 = e % (HD / 8);
             const size_t at = size_t(p0 + j) * HD + 8 * c8;
             *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgh + at);
             *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgl + at);
         }
-        for (int e = tid; e < HD * AK / 8; e += kThreads) {
+        for (int e = tid; e < HD * AK / 8; e += NT) {
             const int d = e / (AK / 8), c8 = e % (AK / 8);
             const size_t at = size_t(d) * t_pad + p0 + 8 * c8;
             *reinterpret_cast<uint4 *>(&vsh[d][8 * c8]) = *reinterpret_cast<const uint4 *>(vgh + at);
@@ -620,8 +623,8 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_f16(
             for (int nt = 0; nt < 4; nt++) {
                 const float e = sc[nt][v] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[nt][v] - mn);
                 const _Float16 hi = (_Float16)e;
-                psh[wave][4 * lg + v][16 * nt + li] = hi;
-                psl[wave][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
+                psh[wave_all][4 * lg + v][16 * nt + li] = hi;
+                psl[wave_all][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
                 sum += e;
             }
             l[v] = l[v] * corr[v] + row16_sum(sum);
@@ -632,13 +635,15 @@ __global__ __launch_bounds__(kThreads) void attention_prefill_f16(
 #pragma unroll
             for (int v = 0; v < 4; v++)
                 o[dt][v] *= corr[v];
-        // P rows of this wave are written and read by this wave only
-        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): LDS writes done
+        // P rows of this wave are written and read by this wave only (LDS
+        // runs a wave's accesses in order; the fences keep the compiler's)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int kb = 0; kb < AK / 32; kb++) {
-            const half8 ah = *reinterpret_cast<const half8 *>(&psh[wave][li][32 * kb + 8 * lg]);
-            const half8 al = *reinterpret_cast<const half8 *>(&psl[wave][li][32 * kb + 8 * lg]);
+            const half8 ah = *reinterpret_cast<const half8 *>(&psh[wave_all][li][32 * kb + 8 * lg]);
+            const half8 al = *reinterpret_cast<const half8 *>(&psl[wave_all][li][32 * kb + 8 * lg]);
 #pragma unroll
             for (int dt = 0; dt < HD / 16; dt++) {
                 const half8 bh = *reinterpret_cast<const half8 *>(&vsh[16 * dt + li][32 * kb + 8 * lg]);
@@ -759,18 +764,31 @@ void launch_attention_prefill(const float *q, const float *k_cache,
     const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
     _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
     const dim3 kv_grid(s.kv_heads, t_pad / AK), grid(s.heads, t_pad / AQ);
+    // two query heads per workgroup when they share a KV head
+    const bool pair = (s.heads / s.kv_heads) % 2 == 0;
+    const dim3 pair_grid(s.heads / 2, t_pad / AQ);
     if (s.head_dim == 128) {
         hipLaunchKernelGGL(kv_limbs_kernel<128>, kv_grid, dim3(kThreads), 0, stream, k_cache,
                            v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
-        hipLaunchKernelGGL(attention_prefill_f16<128>, grid, dim3(kThreads), 0, stream, q,
-                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad, s.heads,
-                           s.kv_heads, s.attn_scale);
+        if (pair)
+            hipLaunchKernelGGL((attention_prefill_f16<128, 2>), pair_grid, dim3(512), 0, stream,
+                               q, k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                               s.heads, s.kv_heads, s.attn_scale);
+        else
+            hipLaunchKernelGGL((attention_prefill_f16<128, 1>), grid, dim3(256), 0, stream, q,
+                               k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                               s.heads, s.kv_heads, s.attn_scale);
     } else {
         hipLaunchKernelGGL(kv_limbs_kernel<64>, kv_grid, dim3(kThreads), 0, stream, k_cache,
                            v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
-        hipLaunchKernelGGL(attention_prefill_f16<64>, grid, dim3(kThreads), 0, stream, q,
-                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad, s.heads,
-                           s.kv_heads, s.attn_scale);
+        if (pair)
+            hipLaunchKernelGGL((attention_prefill_f16<64, 2>), pair_grid, dim3(512), 0, stream,
+                               q, k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                               s.heads, s.kv_heads, s.attn_scale);
+        else
+            hipLaunchKernelGGL((attention_prefill_f16<64, 1>), grid, dim3(256), 0, stream, q,
+                               k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                               s.heads, s.kv_heads, s.attn_scale);
     }
     check_launch("prefill attention");
 }
