@@ -91,6 +91,25 @@ def long_prompt(args, nut, workloads):
     cfg = model.config
     if args.path == "steps":
         dev.set_path(nut.PATH_STEPS)
+    if args.prefill_only:
+        # the batched prefill alone (no decode loop, no captured graph), for
+        # kernel traces of the prefill kernels
+        cache = nut.KVCache(cfg)
+        times = []
+        for i in range(args.warmup + args.steps):
+            t0 = time.time()
+            dev.prefill(cache, prompt)
+            if i >= args.warmup:
+                times.append(time.time() - t0)
+        prefill_s = statistics.median(times)
+        print(json.dumps({
+            "workload": args.workload, "prompt_tokens": len(prompt),
+            "steps": args.steps, "warmup": args.warmup, "prefill_only": True,
+            "prefill_tok_s": round(len(prompt) / prefill_s, 1),
+            "prefill_ms": round(prefill_s * 1e3, 2), "dtype": "fp32",
+            "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        }), flush=True)
+        return
     for _ in range(args.warmup):
         dev.generate(prompt, gen)
     pre, dec, toks, dms = [], [], 0, []
@@ -132,6 +151,9 @@ def main():
                     help="tinyllama_int4 (default): the headline line below; "
                          "the others print one line of prefill and decode "
                          "tok/s for the long-prompt configurations")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="long-prompt workloads: time the batched prefill "
+                         "alone (host clock), for kernel traces")
     ap.add_argument("--path", default="auto", choices=["auto", "steps"],
                     help="steps: eager per-token step kernels only (no token "
                          "kernel, batched prefill or graph replay), for "
