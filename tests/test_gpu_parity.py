@@ -240,6 +240,37 @@ def test_tinyllama_int4_paths_greedy(gpu, tinyllama_int4, path):
     dev.set_path(0)
 
 
+def test_tinyllama_int8_token_kernel_short_context(gpu):
+    """The INT8 token kernel within its fused attention pass (44 positions):
+    a 5-token prompt decoded token by token by the kernel's prefill loop,
+    then 16 greedy ids, against the oracle; hidden states and K/V rows
+    within rel-L2 1e-5."""
+    O.orc().orc_set_threads(16)
+    model = W.build("tinyllama", 0, 3, 64)
+    c = model.config
+    prompt = gpu.synth_tokens(3, c.vocab_size, 5)
+    dev = model.to_device()
+    om = O.oracle_model(model)
+    try:
+        dev.set_path(2)
+        cache = gpu.KVCache(c)
+        h = dev.prefill(cache, prompt)
+        assert rel_l2(h, om.prefill(prompt)) <= TOL
+        h2 = dev.decode(cache, 11)
+        assert rel_l2(h2, om.decode(11)) <= TOL
+        for layer in (0, c.layers - 1):
+            for kvh in range(c.kv_heads):
+                k, v = cache.key_value(layer, kvh, len(prompt))
+                rk, rv = om.kv_row(layer, kvh, len(prompt))
+                assert rel_l2(k, rk) <= TOL and rel_l2(v, rv) <= TOL
+        ids, _ = dev.generate(prompt, 16)
+        ref, _, _ = om.generate(prompt, 16)
+        assert ids == ref
+    finally:
+        dev.set_path(0)
+        dev.close()
+
+
 @pytest.mark.parametrize("scale", [300.0, 1e-30], ids=["outliers", "tiny_dims"])
 def test_token_kernel_wide_range_activations(gpu, scale):
     """Every 257th embedding dimension scaled by 300 (outlier features, as in
