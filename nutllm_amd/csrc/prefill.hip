@@ -764,20 +764,15 @@ void launch_attention_prefill(const float *q, const float *k_cache,
     const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
     _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
     const dim3 kv_grid(s.kv_heads, t_pad / AK), grid(s.heads, t_pad / AQ);
-    // two query heads per workgroup when they share a KV head
+    // head_dim 64: two query heads per workgroup when they share a KV head
     const bool pair = (s.heads / s.kv_heads) % 2 == 0;
     const dim3 pair_grid(s.heads / 2, t_pad / AQ);
     if (s.head_dim == 128) {
         hipLaunchKernelGGL(kv_limbs_kernel<128>, kv_grid, dim3(kThreads), 0, stream, k_cache,
                            v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
-        if (pair)
-            hipLaunchKernelGGL((attention_prefill_f16<128, 2>), pair_grid, dim3(512), 0, stream,
-                               q, k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
-                               s.heads, s.kv_heads, s.attn_scale);
-        else
-            hipLaunchKernelGGL((attention_prefill_f16<128, 1>), grid, dim3(256), 0, stream, q,
-                               k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
-                               s.heads, s.kv_heads, s.attn_scale);
+        hipLaunchKernelGGL((attention_prefill_f16<128, 1>), grid, dim3(256), 0, stream, q,
+                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                           s.heads, s.kv_heads, s.attn_scale);
     } else {
         hipLaunchKernelGGL(kv_limbs_kernel<64>, kv_grid, dim3(kThreads), 0, stream, k_cache,
                            v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
