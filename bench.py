@@ -35,7 +35,7 @@ PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 # HBM bytes one generate launch (16 iterations) moves, from rocprofv3
 # counter runs of this bench: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB (the
 # scales read off a 1 GiB device-to-device copy in the same runs).
-MEASURED_TRAFFIC_BYTES = 13_530_846_208
+MEASURED_TRAFFIC_BYTES = 13_535_426_731
 CPU_SAMPLE_SECONDS = 10.0
 
 
