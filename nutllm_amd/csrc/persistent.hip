@@ -187,6 +187,10 @@ __device__ __forceinline__ void dma_wait()
 
 // Rows [0, n) of 64-float rows at src into LDS rows of 68 floats (16 data
 // granules + 1 spare): LDS granule j holds row j / 17, granule j % 17.
+// POLICY is the loads' cache policy: 0 where every workgroup stages the
+// same rows (they stay in L2), kStreamPolicy where each row is staged by one
+// workgroup once per token.
+template <int POLICY = 0>
 __device__ __forceinline__ void dma_padded_rows(float *lds_dst,
                                                 const float *src, int n)
 {
@@ -201,7 +205,7 @@ __device__ __forceinline__ void dma_padded_rows(float *lds_dst,
                     src + row * 64 + g * 4),
                 (__attribute__((address_space(3))) void *)(
                     reinterpret_cast<char *>(lds_dst) + i * 1024),
-                16, 0, 0);
+                16, 0, POLICY);
     }
 }
 
@@ -1099,8 +1103,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 const int hist = max(0, min(ap1, pos) - ap0); // rows already cached
                 if (hist > 0) {
                     const size_t row0 = size_t(ag) * a.max_seq + ap0;
-                    dma_padded_rows(kst, kc + row0 * G::HD, hist);
-                    dma_padded_rows(vst, vc + row0 * G::HD, hist);
+                    dma_padded_rows<kStreamPolicy>(kst, kc + row0 * G::HD, hist);
+                    dma_padded_rows<kStreamPolicy>(vst, vc + row0 * G::HD, hist);
                 }
             } else if (pos > 0) {
                 for (int kvh = 0; kvh < G::KVH; kvh++) {
