@@ -101,6 +101,8 @@ def long_prompt(args, nut, workloads):
             dev.prefill(cache, prompt)
             if i >= args.warmup:
                 times.append(time.time() - t0)
+        cache.close()
+        dev.close()
         prefill_s = statistics.median(times)
         print(json.dumps({
             "workload": args.workload, "prompt_tokens": len(prompt),
@@ -119,7 +121,14 @@ def long_prompt(args, nut, workloads):
         dec.append(st.decode_seconds)
         dms.append(dev.last_decode_ms())
         toks += st.generated_tokens
+    dev.close()
     n = len(ids)
+    # the greedy ids the reference generated for this run (tests/golden)
+    golden = os.path.join(ROOT, "tests", "golden", f"{args.workload}.npz")
+    ref_ids = None
+    if os.path.exists(golden):
+        import numpy as np
+        ref_ids = np.load(golden)["ids"].tolist()
     prefill_s = statistics.median(pre)
     linear = sum(2 * r * c for r, c in nut.projection_shapes(cfg).values())
     kv = cfg.kv_heads or cfg.heads
@@ -135,6 +144,7 @@ def long_prompt(args, nut, workloads):
         "decode_device_us_per_token": round(statistics.median(dms) * 1e3 / n, 1),
         "kv_heads": kv, "dtype": "fp32",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        "ids_match_reference": None if ref_ids is None else ids == ref_ids,
     }), flush=True)
 
 
@@ -197,6 +207,7 @@ def main():
         tokens += st.generated_tokens
     nut.synchronize()
     t1 = time.perf_counter()
+    dev.close()
 
     value = tokens / sum(decode_s)
     n = len(ids)

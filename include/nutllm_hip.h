@@ -229,6 +229,16 @@ int nut_model_record_timeline(nut_model *m, int mode);
 int nut_model_timeline(const nut_model *m, uint64_t *ticks, size_t capacity,
                        size_t *count);
 
+/* Exchange-tag schedule of the cooperative token kernel (no reference
+ * counterpart). Every launch polls words tagged with its own base; a base
+ * is never 0 and never repeats until the exchange buffer has been zeroed.
+ * nut_token_tag_base advances *launch_count and returns the next launch's
+ * base, with *clear = 1 when the buffer must be zeroed first (the counter
+ * ran out and restarted); it needs no GPU. nut_model_set_launch_count
+ * presets a model's counter (a test hook, to cross the restart quickly). */
+int nut_token_tag_base(unsigned *launch_count, unsigned *base, int *clear);
+int nut_model_set_launch_count(nut_model *m, unsigned launch_count);
+
 /* Device time (HIP events on the model's stream) of the decode loop of the
  * last nut_generate_greedy call: every classifier, argmax and decode step
  * after the prefill. (No reference counterpart: GenerationStats carries

@@ -126,6 +126,8 @@ _SIGS = {
     "nut_model_record_timeline": (C.c_int, [_P, C.c_int]),
     "nut_model_timeline": (C.c_int, [_P, _P, _SZ, _P]),
     "nut_model_destroy": (C.c_int, [_P]),
+    "nut_token_tag_base": (C.c_int, [_P, _P, _P]),
+    "nut_model_set_launch_count": (C.c_int, [_P, C.c_uint]),
     "nut_kv_create": (C.c_int, [_P, _P]),
     "nut_kv_destroy": (C.c_int, [_P]),
     "nut_kv_length": (_SZ, [_P]),
@@ -209,6 +211,16 @@ def synth_tokens(seed, vocab, count):
     out = np.empty(count, np.int32)
     check(lib().nut_synth_tokens(seed, vocab, _ptr(out), count))
     return out
+
+
+def token_tag_base(launch_count):
+    """Next exchange-tag base after launch_count: (base, new count, clear)."""
+    count = C.c_uint(launch_count)
+    base = C.c_uint()
+    clear = C.c_int()
+    check(lib().nut_token_tag_base(C.byref(count), C.byref(base),
+                                   C.byref(clear)))
+    return base.value, count.value, bool(clear.value)
 
 
 # ---------------------------------------------------------------- device --
@@ -470,6 +482,10 @@ class DeviceModel:
         t = t[:, :iterations]
         t = (t - t[0, 0, 0]) / 100.0  # 100 MHz ticks -> us
         return t[0] if wgs == 1 else t
+
+    def set_launch_count(self, count):
+        """Preset the token kernel's launch counter (test hook)."""
+        check(lib().nut_model_set_launch_count(self.handle, count))
 
     def last_decode_ms(self):
         """Device time of the last generate() decode loop (HIP events)."""

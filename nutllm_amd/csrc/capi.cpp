@@ -317,6 +317,27 @@ int nut_model_last_decode_ms(const nut_model *m, double *milliseconds)
     });
 }
 
+int nut_token_tag_base(unsigned *launch_count, unsigned *base, int *clear)
+{
+    return nut::guarded([&]() {
+        nut::require(launch_count != nullptr && base != nullptr && clear != nullptr,
+                     NUT_EINVAL, "tag schedule: null pointer");
+        bool c = false;
+        *base = nut::next_tag_base(*launch_count, c);
+        *clear = c ? 1 : 0;
+    });
+}
+
+int nut_model_set_launch_count(nut_model *m, unsigned launch_count)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::require(launch_count <= nut::kTagBases, NUT_EINVAL,
+                     "tag schedule: launch count beyond the tag range");
+        m->launch_count = launch_count;
+    });
+}
+
 size_t nut_model_storage_bytes(const nut_model *m)
 {
     return m == nullptr ? 0 : nut::storage_bytes(*m);

@@ -543,7 +543,12 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.tokens_out = m.tokens.as<int>();
     a.state = m.state.as<StepState>();
     a.error = m.token_error.as<int>();
-    a.tag_base = (++m.launch_count) << 20;
+    bool clear = false;
+    a.tag_base = next_tag_base(m.launch_count, clear);
+    if (clear)
+        hip_check(hipMemsetAsync(m.exchange.get(), 0,
+                                 token_exchange_entries(s) * sizeof(uint64_t), m.stream),
+                  "hipMemsetAsync");
     a.layer_count = int(m.config.layers);
     a.vocab = s.vocab;
     a.max_seq = s.max_seq;

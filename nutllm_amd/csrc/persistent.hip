@@ -1345,6 +1345,8 @@ void launch_as(const TokenArgs &args, hipStream_t stream)
             "token kernel: grid does not fit the device");
     require(args.start_len + args.n_iter <= (LONG ? G::SPLITS * G::PMAX : G::NP), NUT_EINVAL,
             "token kernel: context exceeds the attention pass");
+    require(token_tags_needed(args.n_iter, args.layer_count) <= (1ll << kTagShift), NUT_EINVAL,
+            "token kernel: launch exceeds its exchange tag range");
     require(!LONG || (args.x_apart != nullptr && args.x_ctx != nullptr), NUT_EINVAL,
             "token kernel: split attention needs its exchange buffers");
     TokenArgs a = args;

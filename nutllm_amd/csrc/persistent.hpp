@@ -34,7 +34,7 @@ struct TokenArgs {
     int *tokens_out;          // emitted tokens (generate)
     StepState *state;
     int *error;               // set on a bounded-wait timeout
-    unsigned tag_base;        // unique per launch (launch counter << 20)
+    unsigned tag_base;        // next_tag_base: unique since the last clear
     // Optional phase timeline (s_memrealtime ticks, 100 MHz) of workgroups
     // [0, timeline_wgs): marks_per_iteration(layers) entries per iteration,
     // timeline_cap entries per workgroup.
@@ -44,6 +44,33 @@ struct TokenArgs {
     int start_len, n_iter, classify;
     float attn_scale;
 };
+
+// Exchange tags. Every exchange word is (tag << 32) | value, and a launch
+// uses the tags [base, base + 2^kTagShift) with base = count << kTagShift for
+// a launch counter count in 1 .. kTagBases. A word in the buffer carries
+// either tag 0 (the buffer was zeroed) or a tag of a launch since the last
+// zeroing; bases are never 0 and never repeat between zeroings, so no
+// consumer can find a stale word already holding the tag it waits for. When
+// the counter runs out, next_tag_base asks for the buffer to be zeroed
+// before the launch and restarts it at 1.
+constexpr unsigned kTagShift = 20;
+constexpr unsigned kTagBases = (1u << (32 - kTagShift)) - 1;
+
+inline unsigned next_tag_base(unsigned &count, bool &clear)
+{
+    clear = count >= kTagBases;
+    if (clear)
+        count = 0;
+    return (++count) << kTagShift;
+}
+
+// Tags one launch may use: per iteration one for the argmax exchange, then
+// per layer at most six (q/k/v, two for split attention, h after Wo, act,
+// h after W2).
+inline long long token_tags_needed(long long n_iter, long long layers)
+{
+    return n_iter * (1 + 6 * layers) + 1;
+}
 
 // Timeline entries per iteration: iteration start, token known, then per
 // layer, for each of the phases A, B, C, D: input staged, outputs published

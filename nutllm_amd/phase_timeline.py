@@ -64,12 +64,18 @@ def main(argv):
     name = argv[1] if len(argv) > 1 else "tinyllama_int4"
     model, prompt, gen = workloads.build_run(name)
     dev = model.to_device()
-    dev.generate(prompt, gen)
-    dev.record_timeline(2)
-    ids, _ = dev.generate(prompt, gen)
-    n = len(ids)
-    t = dev.timeline(n)
-    print(f"{name}: {n} tokens, {dev.last_decode_ms() * 1e3 / n:.1f} us per token (HIP events)")
+    try:
+        dev.generate(prompt, gen)
+        dev.record_timeline(2)
+        ids, _ = dev.generate(prompt, gen)
+        n = len(ids)
+        t = dev.timeline(n)
+        ms = dev.last_decode_ms()
+    finally:
+        # the model's graph, stream and buffers go before the HIP runtime's
+        # own exit handlers run
+        dev.close()
+    print(f"{name}: {n} tokens, {ms * 1e3 / n:.1f} us per token (HIP events)")
     for key, v in summarise(t, model.config.layers).items():
         print(f"  {key:24s} {v:6.2f} us")
 

@@ -14,6 +14,10 @@ src/attention.cpp:37-38), quantised by the product quantiser:
 Streams of nut_synth_normal: embeddings 1, classifier 2, projection p of
 layer l: 16 + 8 l + p (p in query, key, value, output, gate, up, down).
 eos_token is 1, as the llama2.c adapter sets (src/llama2.cpp:222-223).
+
+``build(..., norm_seed=s)`` replaces the unit norm weights with seeded
+N(1, 0.25^2) vectors (attention and ffn norm of every layer, and the final
+norm), so that tests see every norm weight enter the computation.
 """
 from __future__ import annotations
 
@@ -41,6 +45,10 @@ SHAPES = {
     "llama7b": dict(layers=32, heads=32, dim=4096, head_dim=128,
                     ffn_dim=11008, vocab_size=32000, max_seq=640,
                     eos_token=1, kv_heads=32),
+    # the Llama-2-7B widths with two layers, for oracle parity at full width
+    "llama7b_2l": dict(layers=2, heads=32, dim=4096, head_dim=128,
+                       ffn_dim=11008, vocab_size=32000, max_seq=640,
+                       eos_token=1, kv_heads=32),
     # small shapes for the step-kernel parity tests: head_dim 128 with one
     # query head per KV head, head_dim 64 with four and with two
     "step_mha128": dict(layers=2, heads=2, dim=256, head_dim=128, ffn_dim=512,
@@ -84,6 +92,8 @@ class SynthModel:
     final_norm: np.ndarray
     lm_head: np.ndarray
     layers: list = field(default_factory=list)  # name -> (data, scales, r, c)
+    # per layer (attention_norm, ffn_norm); None means all ones
+    norms: list | None = None
 
     def layer_fp32(self, layer):
         """The layer's fp32 projections, regenerated from the seed."""
@@ -93,14 +103,18 @@ class SynthModel:
                                      rows * cols, SIGMA).reshape(rows, cols)
         return out
 
-    def norm(self):
-        return np.ones(self.config.dim, np.float32)
+    def layer_norms(self, layer):
+        """(attention_norm, ffn_norm) of a layer."""
+        if self.norms is not None:
+            return self.norms[layer]
+        ones = np.ones(self.config.dim, np.float32)
+        return ones, ones
 
     def to_device(self):
         m = DeviceModel(self.config, self.qtype)
         m.set_globals(self.embeddings, self.final_norm, self.lm_head)
         for i, mats in enumerate(self.layers):
-            m.set_layer(i, mats, self.norm(), self.norm())
+            m.set_layer(i, mats, *self.layer_norms(i))
         return m
 
     def weight_bytes_per_token(self):
@@ -114,8 +128,18 @@ class SynthModel:
                 (2 * c.layers + 1) * c.dim * 4 + c.dim * 4)
 
 
-def build(shape, qtype, seed, max_seq=None, keep_fp32=False):
-    """Generate and quantise a synthetic model (host arrays)."""
+def seeded_norms(seed, dim, layers):
+    """Per-layer (attention, ffn) norm weights and a final norm, N(1, 0.25^2)
+    from numpy's default_rng(seed)."""
+    rng = np.random.default_rng(seed)
+    draw = lambda: (1.0 + 0.25 * rng.standard_normal(dim)).astype(np.float32)  # noqa: E731
+    per_layer = [(draw(), draw()) for _ in range(layers)]
+    return per_layer, draw()
+
+
+def build(shape, qtype, seed, max_seq=None, keep_fp32=False, norm_seed=None):
+    """Generate and quantise a synthetic model (host arrays); norm_seed
+    draws non-unit norm weights (seeded_norms)."""
     cfg = make_config(shape, max_seq)
     n = cfg.vocab_size * cfg.dim
     emb = synth_normal(seed, STREAM_EMBED, n, SIGMA).reshape(cfg.vocab_size,
@@ -124,6 +148,9 @@ def build(shape, qtype, seed, max_seq=None, keep_fp32=False):
         cfg.vocab_size, cfg.dim)
     model = SynthModel(cfg, qtype, seed, emb, np.ones(cfg.dim, np.float32),
                        head)
+    if norm_seed is not None:
+        model.norms, model.final_norm = seeded_norms(norm_seed, cfg.dim,
+                                                     cfg.layers)
     fp32 = []
     for layer in range(cfg.layers):
         weights = model.layer_fp32(layer)

@@ -244,7 +244,8 @@ def oracle_model(synth):
     """OracleModel over a nutllm_amd.workloads.SynthModel's arrays."""
     cfg = {n: getattr(synth.config, n) for n, _ in OrcConfig._fields_}
     return OracleModel(cfg, synth.qtype, synth.embeddings, synth.final_norm,
-                       synth.lm_head, synth.layers)
+                       synth.lm_head, synth.layers,
+                       getattr(synth, "norms", None))
 
 
 class RefModel:
@@ -286,14 +287,16 @@ class RefModel:
         self.dim = c.dim
         self.vocab = c.vocab_size
         ones = np.ones(c.dim, np.float32)
-        for mats in synth.layers:
+        norms = getattr(synth, "norms", None)
+        for i, mats in enumerate(synth.layers):
             data = (C.c_void_p * 7)(*[mats[n][0].ctypes.data
                                       for n in PROJECTIONS])
             scales = (C.c_void_p * 7)(*[mats[n][1].ctypes.data
                                         for n in PROJECTIONS])
+            an, fn = norms[i] if norms else (ones, ones)
             check(ref().ref_model_add_layer_quantized(self.handle, data,
-                                                      scales, ptr(ones),
-                                                      ptr(ones)),
+                                                      scales, ptr(an),
+                                                      ptr(fn)),
                   "ref_model_add_layer_quantized")
         return self
 

@@ -20,7 +20,12 @@ Files written:
                   greedy ids (16), per-step hidden states, final-step
                   logits, KV cache contents
   tinyllama_int4.json  greedy ids of the TinyLlama-shape INT4 run
-                  (5-token prompt, 16 tokens)
+                  (5-token prompt, 16 tokens) and its storage_bytes
+  tinyllama_int8_2k.npz, llama7b_int4.npz
+                  the long-prompt runs (TinyLlama-shape INT8, 2048-token
+                  prompt, 128 tokens; Llama-2-7B-shape INT4, 512-token
+                  prompt, 128 tokens): greedy ids, the hidden state after
+                  the prompt, sampled K/V cache rows, storage_bytes
 
 Also copied verbatim (data files the reference's tests hold):
   tiny-llama2.bin, tiny-llama2-shared.bin   (tests/fixtures/)
@@ -193,12 +198,14 @@ def write_tiny(qtype, tag):
     kv = oracle.orc().orc_kv_elements(oracle.C.byref(oracle.OrcConfig(**cfg)))
     hidden, keys, values = ref.decode_trace(tokens, kv_elements=kv)
     logits = ref.logits(hidden[len(prompt) - 1])
+    storage = ref.storage_bytes()
     ref.close()
     np.savez_compressed(
         os.path.join(HERE, f"tiny_{tag}.npz"), prompt=prompt,
         ids=np.array(ids, np.int32), tokens=tokens, hidden=hidden,
         logits=logits, keys=keys, values=values,
-        digest=np.array(weight_digest(model)))
+        digest=np.array(weight_digest(model)),
+        storage_bytes=np.int64(storage))
 
 
 def write_tinyllama():
@@ -209,10 +216,49 @@ def write_tinyllama():
     ref = oracle.RefModel(cfg, INT4, model.embeddings, model.final_norm,
                           model.lm_head, layers)
     ids, _, _ = ref.generate(prompt, gen, threads=8)
+    storage = ref.storage_bytes()
     ref.close()
     with open(os.path.join(HERE, "tinyllama_int4.json"), "w") as f:
         json.dump({"run": "tinyllama_int4", "prompt": prompt.tolist(),
-                   "ids": ids, "digest": weight_digest(model)}, f, indent=1)
+                   "ids": ids, "digest": weight_digest(model),
+                   "storage_bytes": storage}, f, indent=1)
+
+
+def kv_sample(c, n):
+    """(layer, kv head, position) rows kept from a long run's cache."""
+    kvh = c.kv_heads or c.heads
+    return np.array([(l, h, p) for l in sorted({0, c.layers // 2, c.layers - 1})
+                     for h in sorted({0, kvh - 1})
+                     for p in sorted({0, n // 2, n - 1})], np.int64)
+
+
+def write_long(name):
+    """A long-prompt run through the reference's own path over the product
+    quantiser's storage (bit-identical to QuantizedMatrix::quantize, pinned
+    by quant.npz): its greedy generate_tokens_cached ids, and from a
+    decode trace of the prompt the last hidden state and sampled K/V rows."""
+    model, prompt, gen = W.build_run(name)
+    c = model.config
+    cfg = {n: getattr(c, n) for n, _ in oracle.OrcConfig._fields_}
+    kv = oracle.orc().orc_kv_elements(oracle.C.byref(oracle.OrcConfig(**cfg)))
+    ref = oracle.RefModel.from_quantized(model)
+    threads = min(8, os.cpu_count() or 1)
+    hidden, keys, values = ref.decode_trace(prompt, threads, kv_elements=kv)
+    ids, pre, dec = ref.generate(prompt, gen, threads=threads)
+    storage = ref.storage_bytes()
+    ref.close()
+    rows = kv_sample(c, len(prompt))
+    kvh = c.kv_heads or c.heads
+    offs = [((l * kvh + h) * c.max_seq + p) * c.head_dim for l, h, p in rows]
+    k_rows = np.stack([keys[o:o + c.head_dim] for o in offs])
+    v_rows = np.stack([values[o:o + c.head_dim] for o in offs])
+    np.savez_compressed(
+        os.path.join(HERE, f"{name}.npz"), prompt=prompt,
+        ids=np.array(ids, np.int32), hidden=hidden[-1], kv_index=rows,
+        keys=k_rows, values=v_rows, digest=np.array(weight_digest(model)),
+        storage_bytes=np.int64(storage))
+    print(f"{name}: {len(ids)} ids, prefill {pre:.1f} s, decode {dec:.1f} s "
+          f"({threads} threads)", flush=True)
 
 
 def copy_fixtures():
@@ -224,6 +270,10 @@ def copy_fixtures():
 def main():
     if not oracle.ref_available():
         sys.exit("oracle/_ref/libnutref.so is not built: make -C oracle ref")
+    if "--only-long" in sys.argv:
+        for name in ("tinyllama_int8_2k", "llama7b_int4"):
+            write_long(name)
+        return
     write_quant()
     write_quant_errors()
     write_tiny(INT8, "int8")
@@ -231,6 +281,9 @@ def main():
     copy_fixtures()
     if "--skip-tinyllama" not in sys.argv:
         write_tinyllama()
+    if "--long" in sys.argv:
+        for name in ("tinyllama_int8_2k", "llama7b_int4"):
+            write_long(name)
 
 
 if __name__ == "__main__":

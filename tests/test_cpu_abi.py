@@ -122,3 +122,28 @@ def test_device_calls_fail_loudly_without_gpu():
     data, scales = nut.quantize(np.ones((4, 32), np.float32), 0)
     with pytest.raises(nut.DeviceError):
         nut.QWeight(data, scales, 4, 32, 0)
+
+
+def test_token_tag_schedule_never_reuses_a_live_base():
+    """The token kernel's exchange words carry (tag << 32) | value and each
+    launch polls for tags of its own base. Over three restarts of the
+    32-bit tag range (every launch kind uses the same counter): no base is
+    0 (the tag of zeroed words), no base repeats since the last zeroing,
+    and a zeroing is asked for exactly when the counter restarts, so a word
+    left by an earlier launch can never already hold the tag a consumer of
+    a later launch waits for."""
+    count = 0
+    live = set()  # bases launched since the buffer was last zeroed
+    clears = 0
+    for _ in range(3 * 4095 + 10):
+        base, count, clear = nut.token_tag_base(count)
+        if clear:
+            clears += 1
+            live.clear()
+        assert base != 0 and base % (1 << 20) == 0
+        assert base not in live
+        live.add(base)
+    assert clears == 3
+    # a preset counter (the GPU test hook) restarts on its next launch
+    assert nut.token_tag_base(4095) == (1 << 20, 1, True)
+    assert nut.token_tag_base(4094) == (4095 << 20, 4095, False)
