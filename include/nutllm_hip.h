@@ -188,6 +188,19 @@ int nut_kv_store(nut_kvcache *kv, size_t layer, size_t position,
  * every layer at position = length; writes the pre-final-norm hidden state
  * [dim] to hidden (host, may be NULL) and increments the length. */
 int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden);
+/* nut_decode without allocating (no reference counterpart): for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid it). Same validation and result as
+ * nut_decode on the step kernels (NUT_PATH_STEPS); the split-attention
+ * partials and arrival counters live in a per-device 2 MiB scratch array
+ * instead of model-owned allocations, and the hidden state goes to the
+ * device pointer d_hidden (may be NULL). Limit: heads x splits x
+ * (head_dim + 2) words of 8 bytes plus 2 x heads counters must fit 2 MiB,
+ * else NUT_EINVAL (TinyLlama needs 0.55 MiB, Llama-2-7B 0.27). Every call
+ * on one GPU shares that GPU's array and clears it first: calls that
+ * overlap on one GPU (other host threads, other streams) race. */
+int nut_decode_noalloc(nut_model *m, nut_kvcache *kv, int token,
+                       float *d_hidden);
 /* prefill_quantized (src/quant_model.cpp:208-220): resets the cache and
  * runs the prompt; hidden gets the last token's hidden state. */
 int nut_prefill(nut_model *m, nut_kvcache *kv, const int *tokens,

@@ -139,6 +139,7 @@ _SIGS = {
     "nut_kv_read": (C.c_int, [_P, _SZ, _SZ, _SZ, _P, _P]),
     "nut_kv_store": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
     "nut_decode": (C.c_int, [_P, _P, C.c_int, _P]),
+    "nut_decode_noalloc": (C.c_int, [_P, _P, C.c_int, _P]),
     "nut_prefill": (C.c_int, [_P, _P, _P, _SZ, _P]),
     "nut_logits": (C.c_int, [_P, _P, _P]),
     "nut_generate_greedy": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
@@ -498,6 +499,12 @@ class DeviceModel:
         check(lib().nut_decode(self.handle, cache.handle, int(token),
                                _ptr(hidden)))
         return hidden
+
+    def decode_noalloc(self, cache, token, out):
+        """nut_decode_noalloc: the hidden state lands in the DeviceArray
+        `out` (dim floats, or None)."""
+        check(lib().nut_decode_noalloc(self.handle, cache.handle, int(token),
+                                       None if out is None else out.ptr))
 
     def prefill(self, cache, tokens):
         t = np.ascontiguousarray(tokens, np.int32)

@@ -452,6 +452,16 @@ int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden)
     });
 }
 
+int nut_decode_noalloc(nut_model *m, nut_kvcache *kv, int token, float *d_hidden)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && kv != nullptr, NUT_EINVAL,
+                     "quantized decode: null pointer");
+        nut::ensure_device();
+        nut::decode_noalloc(*m, *kv, token, d_hidden);
+    });
+}
+
 int nut_prefill(nut_model *m, nut_kvcache *kv, const int *tokens, size_t count,
                 float *hidden)
 {

@@ -3,6 +3,7 @@
 // generation). Validation and messages follow the reference's exceptions
 // (src/quant_model.cpp:161-172,212-213; src/generate.cpp:177-181).
 #include "model.hpp"
+#include "noalloc.hpp"
 #include "persistent.hpp"
 #include "prefill.hpp"
 
@@ -603,6 +604,53 @@ void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden)
                   "hipMemcpyAsync");
     sync(m);
     check_token_error(m);
+    kv.length += 1;
+}
+
+void decode_noalloc(nut_model &m, nut_kvcache &kv, int token, float *d_hidden)
+{
+    require(config_valid(m.config), NUT_EINVAL, "model config: invalid dimensions");
+    require(kv_compatible(kv, m.config), NUT_EINVAL,
+            "quantized decode: cache configuration mismatch");
+    check_ready(m, "quantized decode");
+    require(token >= 0 && size_t(token) < m.config.vocab_size, NUT_EOUTOFRANGE,
+            "quantized decode: token out of range");
+    require(kv.length < kv.config.max_seq, NUT_ELENGTH,
+            "quantized decode: context is full");
+    require(fast_steps(m), NUT_EINVAL,
+            "no-alloc decode: needs 32-wide quant blocks along whole rows and head_dim "
+            "64 or 128");
+    const DecodeShape &s = m.shape;
+    // one token's split-attention partials (0xff-filled: no word carries a
+    // live tag) and arrival counters (zero), as a fresh model starts them
+    const size_t part_words = step_attn_part_words(s) / kStepTokensMax;
+    const size_t count_ints = 2 * size_t(s.heads);
+    require(part_words * sizeof(uint64_t) + count_ints * sizeof(int) <= kNoAllocScratchBytes,
+            NUT_EINVAL, "no-alloc decode: attention workspace exceeds the 2 MiB scratch");
+    uint8_t *scratch = static_cast<uint8_t *>(noalloc_scratch());
+    uint64_t *parts = reinterpret_cast<uint64_t *>(scratch);
+    int *counts = reinterpret_cast<int *>(scratch + part_words * sizeof(uint64_t));
+    launch_fill_words(reinterpret_cast<uint32_t *>(parts), 0xffffffffu, 2 * part_words,
+                      m.stream);
+    launch_fill_words(reinterpret_cast<uint32_t *>(counts), 0u, count_ints, m.stream);
+    kv.sync_length(m.stream);
+    StepState *state = m.state.as<StepState>();
+    launch_reset_state(state, token, m.stream);
+    launch_embed(s, m.embeddings.as<float>(), &state->token, state, m.hidden.as<float>(),
+                 m.stream);
+    const StepBuffers b{m.hidden.as<float>(), m.query.as<float>(), m.context.as<float>(),
+                        m.act.as<float>(), parts, counts};
+    const size_t layer_elems = kv.layer_elements();
+    for (size_t l = 0; l < m.layers.size(); l++)
+        launch_layer_fast(s, m.layers[l].view, m.rope.as<float2>(),
+                          kv.device_length.as<int>(), kv.keys.as<float>() + l * layer_elems,
+                          kv.values.as<float>() + l * layer_elems, b, 1, state, m.stream);
+    launch_finish_step(state, kv.device_length.as<int>(), m.stream);
+    if (d_hidden != nullptr)
+        hip_check(hipMemcpyAsync(d_hidden, m.hidden.get(), m.config.dim * sizeof(float),
+                                 hipMemcpyDeviceToDevice, m.stream),
+                  "hipMemcpyAsync");
+    sync(m);
     kv.length += 1;
 }
 

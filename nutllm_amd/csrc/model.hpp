@@ -104,6 +104,9 @@ nut_kvcache *create_kv(const nut_config &config);
 bool kv_compatible(const nut_kvcache &kv, const nut_config &config);
 
 void decode(nut_model &m, nut_kvcache &kv, int token, float *hidden);
+// decode on the step kernels with the attention workspace in the
+// per-device scratch array (noalloc.hpp); d_hidden is a device pointer.
+void decode_noalloc(nut_model &m, nut_kvcache &kv, int token, float *d_hidden);
 void prefill(nut_model &m, nut_kvcache &kv, const int *tokens, size_t count,
              float *hidden);
 void logits(nut_model &m, const float *hidden, float *out);
