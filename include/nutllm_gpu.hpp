@@ -18,8 +18,9 @@
 //   * QuantizedModelWeights holds host storage; DeviceModel is its copy in
 //     HBM, built once and passed where the reference passes the weights.
 //   * KVCache lives in HBM; key()/value() return a host copy of the row.
-//   * generate_tokens_cached samples greedily only: temperature > 0 is
-//     rejected with std::invalid_argument.
+//   * generate_tokens_cached samples with temperature / top-p through
+//     nut_generate_sampled (device numerators and sort, the reference's
+//     std::mt19937 draw on the host).
 //   * thread_count is validated as the reference does and otherwise unused.
 // Header-only: link with -lnutllm_hip.
 #pragma once
@@ -378,14 +379,12 @@ inline std::vector<int> generate_tokens_cached(DeviceModel &model,
         throw std::invalid_argument("generation: invalid prompt length");
     if (sampling.threads == 0)
         throw std::invalid_argument("generation: zero threads");
-    if (sampling.temperature > 0.0f)
-        throw std::invalid_argument(
-            "generation: the device path samples greedily (temperature 0)");
     std::vector<int> out(sampling.max_tokens > 0 ? sampling.max_tokens : 1);
     size_t count = 0;
     nut_generation_stats s{};
-    check(nut_generate_greedy(model.handle(), prompt.data(), prompt.size(),
-                              sampling.max_tokens, out.data(), &count, &s));
+    check(nut_generate_sampled(model.handle(), prompt.data(), prompt.size(),
+                               sampling.max_tokens, sampling.temperature, sampling.top_p,
+                               sampling.seed, out.data(), &count, &s));
     out.resize(count);
     if (stats != nullptr) {
         stats->prefill_tokens = s.prefill_tokens;

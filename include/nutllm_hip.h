@@ -181,6 +181,14 @@ int nut_kv_read(const nut_kvcache *kv, size_t layer, size_t head,
 /* KVCache::store: key/value are [kv_heads x head_dim] host vectors. */
 int nut_kv_store(nut_kvcache *kv, size_t layer, size_t position,
                  const float *key, const float *value);
+/* KVCache::key / value / store over a run of positions at once (one
+ * strided copy each way): host arrays [layer][kv_head][end - begin]
+ * [head_dim]. Read-back or upload only: the length is not changed. Either
+ * output of the read may be NULL. */
+int nut_kv_read_positions(const nut_kvcache *kv, size_t begin, size_t end,
+                          float *keys, float *values);
+int nut_kv_write_positions(nut_kvcache *kv, size_t begin, size_t end,
+                           const float *keys, const float *values);
 
 /* -------------------------------------------------------- token loop -- */
 
@@ -215,6 +223,21 @@ int nut_logits(nut_model *m, const float *hidden, float *logits);
 int nut_generate_greedy(nut_model *m, const int *prompt, size_t prompt_len,
                         size_t max_tokens, int *out, size_t *out_count,
                         nut_generation_stats *stats);
+
+/* generate_tokens_cached with SamplingConfig{max_tokens, temperature,
+ * top_p, seed} (src/generate.cpp:31-72,174-216): temperature <= 0 is the
+ * greedy loop above; otherwise each step's logits, softmax numerators
+ * p = exp((logit - max) / temperature) and their sort (p descending, token
+ * ascending) run on the device, and the host walks the sorted prefix with
+ * the reference's sequential nucleus sum and draws with std::mt19937(seed)
+ * and uniform_real_distribution<double>, as choose_token does. Errors as
+ * the reference's: "sampling: invalid temperature or top-p"
+ * (NUT_EINVAL), "sampling: non-finite probability" and "sampling: zero
+ * probability mass" (NUT_ERUNTIME). */
+int nut_generate_sampled(nut_model *m, const int *prompt, size_t prompt_len,
+                         size_t max_tokens, float temperature, float top_p,
+                         uint32_t seed, int *out, size_t *out_count,
+                         nut_generation_stats *stats);
 
 /* Execution path of decode / prefill / generate (no reference counterpart;
  * every path computes the same function): NUT_PATH_AUTO picks the

@@ -143,6 +143,10 @@ _SIGS = {
     "nut_prefill": (C.c_int, [_P, _P, _P, _SZ, _P]),
     "nut_logits": (C.c_int, [_P, _P, _P]),
     "nut_generate_greedy": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+    "nut_generate_sampled": (C.c_int, [_P, _P, _SZ, _SZ, C.c_float, C.c_float,
+                                       C.c_uint32, _P, _P, _P]),
+    "nut_kv_read_positions": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
+    "nut_kv_write_positions": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
 }
 
 
@@ -405,6 +409,21 @@ class KVCache:
                                 _ptr(v)))
         return k, v
 
+    def read_positions(self, begin, end):
+        """K and V rows of positions [begin, end): [layer][kv_head][n][hd]."""
+        c = self.config
+        shape = (c.layers, c.kv_heads or c.heads, end - begin, c.head_dim)
+        k = np.empty(shape, np.float32)
+        v = np.empty(shape, np.float32)
+        check(lib().nut_kv_read_positions(self.handle, begin, end, _ptr(k), _ptr(v)))
+        return k, v
+
+    def write_positions(self, begin, keys, values):
+        k = np.ascontiguousarray(keys, np.float32)
+        v = np.ascontiguousarray(values, np.float32)
+        check(lib().nut_kv_write_positions(self.handle, begin, begin + k.shape[2],
+                                           _ptr(k), _ptr(v)))
+
     def store(self, layer, position, key, value):
         k = np.ascontiguousarray(key, np.float32)
         v = np.ascontiguousarray(value, np.float32)
@@ -528,6 +547,17 @@ class DeviceModel:
         check(lib().nut_generate_greedy(self.handle, _ptr(p), p.size,
                                         max_tokens, _ptr(out),
                                         C.byref(count), C.byref(stats)))
+        return out[:count.value].tolist(), stats
+
+    def generate_sampled(self, prompt, max_tokens, temperature, top_p, seed):
+        """generate_tokens_cached with temperature / top-p sampling."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max(1, max_tokens), np.int32)
+        count = C.c_size_t()
+        stats = GenerationStats()
+        check(lib().nut_generate_sampled(self.handle, _ptr(p), p.size, max_tokens,
+                                         float(temperature), float(top_p), int(seed),
+                                         _ptr(out), C.byref(count), C.byref(stats)))
         return out[:count.value].tolist(), stats
 
     def close(self):

@@ -442,6 +442,75 @@ int nut_kv_store(nut_kvcache *kv, size_t layer, size_t position, const float *ke
     });
 }
 
+namespace {
+
+// Positions [begin, end) of every (layer, kv head) row as one strided copy:
+// host [layer][kv_head][end - begin][head_dim], device rows max_seq apart.
+void kv_rows_copy(nut_kvcache *kv, size_t begin, size_t end, float *keys, float *values,
+                  const float *src_keys, const float *src_values, bool to_host)
+{
+    nut::require(kv != nullptr, NUT_EINVAL, "kv cache: null cache");
+    nut::require(begin <= end && end <= kv->config.max_seq, NUT_EOUTOFRANGE,
+                 "kv cache: index out of range");
+    nut::ensure_device();
+    if (begin == end)
+        return;
+    const size_t hd = kv->config.head_dim;
+    const size_t width = (end - begin) * hd * sizeof(float);
+    const size_t pitch = kv->config.max_seq * hd * sizeof(float);
+    const size_t rows = kv->config.layers * kv->kv_heads();
+    float *dk = kv->keys.as<float>() + begin * hd;
+    float *dv = kv->values.as<float>() + begin * hd;
+    if (to_host) {
+        if (keys != nullptr)
+            nut::hip_check(hipMemcpy2D(keys, width, dk, pitch, width, rows, hipMemcpyDeviceToHost),
+                           "hipMemcpy2D to host");
+        if (values != nullptr)
+            nut::hip_check(hipMemcpy2D(values, width, dv, pitch, width, rows,
+                                       hipMemcpyDeviceToHost),
+                           "hipMemcpy2D to host");
+    } else {
+        nut::require(src_keys != nullptr && src_values != nullptr, NUT_EINVAL,
+                     "kv cache: null source");
+        nut::hip_check(hipMemcpy2D(dk, pitch, src_keys, width, width, rows, hipMemcpyHostToDevice),
+                       "hipMemcpy2D to device");
+        nut::hip_check(hipMemcpy2D(dv, pitch, src_values, width, width, rows,
+                                   hipMemcpyHostToDevice),
+                       "hipMemcpy2D to device");
+    }
+}
+
+} // namespace
+
+int nut_kv_read_positions(const nut_kvcache *kv, size_t begin, size_t end, float *keys,
+                          float *values)
+{
+    return nut::guarded([&]() {
+        kv_rows_copy(const_cast<nut_kvcache *>(kv), begin, end, keys, values, nullptr, nullptr,
+                     true);
+    });
+}
+
+int nut_kv_write_positions(nut_kvcache *kv, size_t begin, size_t end, const float *keys,
+                           const float *values)
+{
+    return nut::guarded([&]() {
+        kv_rows_copy(kv, begin, end, nullptr, nullptr, keys, values, false);
+    });
+}
+
+int nut_generate_sampled(nut_model *m, const int *prompt, size_t prompt_len,
+                         size_t max_tokens, float temperature, float top_p, uint32_t seed,
+                         int *out, size_t *out_count, nut_generation_stats *stats)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "generation: null model");
+        nut::ensure_device();
+        nut::generate_sampled(*m, prompt, prompt_len, max_tokens, temperature, top_p, seed, out,
+                              out_count, stats);
+    });
+}
+
 int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden)
 {
     return nut::guarded([&]() {

@@ -6,11 +6,13 @@
 #include "noalloc.hpp"
 #include "persistent.hpp"
 #include "prefill.hpp"
+#include "sample.hpp"
 
 #include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <random>
 #include <string>
 
 namespace nut {
@@ -797,6 +799,120 @@ void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
                             hipMemcpyDeviceToHost),
                   "hipMemcpy");
     kv.length = prompt_len + count; // every emitted token was decoded
+    *out_count = count;
+    if (stats != nullptr) {
+        stats->prefill_tokens = prompt_len;
+        stats->generated_tokens = count;
+        stats->prefill_seconds = t1 - t0;
+        stats->decode_seconds = t2 - t1;
+    }
+}
+
+void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
+                      size_t max_tokens, float temperature, float top_p, uint32_t seed,
+                      int *out, size_t *out_count, nut_generation_stats *stats)
+{
+    if (temperature <= 0.0f) {
+        // choose_token's greedy branch (src/generate.cpp:28-30)
+        generate_greedy(m, prompt, prompt_len, max_tokens, out, out_count, stats);
+        return;
+    }
+    require(config_valid(m.config), NUT_EINVAL, "model config: invalid dimensions");
+    require(prompt != nullptr && prompt_len != 0 && prompt_len <= m.config.max_seq,
+            NUT_EINVAL, "generation: invalid prompt length");
+    require(out != nullptr || max_tokens == 0, NUT_EINVAL, "generation: null output");
+    require(out_count != nullptr, NUT_EINVAL, "generation: null output");
+    check_ready(m, "generation");
+    if (!m.generation_cache)
+        m.generation_cache.reset(create_kv(m.config));
+    nut_kvcache &kv = *m.generation_cache;
+    const DecodeShape &s = m.shape;
+    const int vocab = s.vocab;
+    if (m.sample_ws.get() == nullptr)
+        m.sample_ws.allocate(sample_workspace_bytes(vocab));
+
+    const double t0 = now();
+    prefill(m, kv, prompt, prompt_len, nullptr);
+    const double t1 = now();
+    // src/generate.cpp:184-207: one mt19937 per call, seeded with the seed
+    std::mt19937 rng(seed);
+    std::vector<float> p;
+    std::vector<int> ids;
+    std::vector<double> totals;
+    constexpr size_t kChunk = 4096;
+    size_t count = 0;
+    StepState *state = m.state.as<StepState>();
+    const int parts = classifier_blocks(s);
+    while (count < max_tokens && kv.length < kv.config.max_seq) {
+        // choose_token's checks (src/generate.cpp:34-36), at its first call
+        require(std::isfinite(temperature) && top_p > 0.0f && top_p <= 1.0f, NUT_EINVAL,
+                "sampling: invalid temperature or top-p");
+        launch_reset_state(state, 0, m.stream);
+        launch_classifier(s, m.hidden.as<float>(), m.final_norm.as<float>(), m.output_weights(),
+                          m.logits.as<float>(), m.part_val.as<float>(), m.part_idx.as<int>(),
+                          state, m.stream);
+        float *sorted_p = nullptr;
+        int *sorted_ids = nullptr, *bad = nullptr;
+        double *block_totals = nullptr;
+        const int nt = sample_sort(m.logits.as<float>(), vocab, m.part_val.as<float>(), parts,
+                                   temperature, m.sample_ws.get(), &sorted_p, &sorted_ids,
+                                   &block_totals, &bad, m.stream);
+        totals.resize(nt);
+        int bad_host = 0;
+        hip_check(hipMemcpyAsync(totals.data(), block_totals, nt * sizeof(double),
+                                 hipMemcpyDeviceToHost, m.stream),
+                  "hipMemcpyAsync");
+        hip_check(hipMemcpyAsync(&bad_host, bad, sizeof bad_host, hipMemcpyDeviceToHost,
+                                 m.stream),
+                  "hipMemcpyAsync");
+        sync(m);
+        if (bad_host != 0)
+            fail(NUT_ERUNTIME, "sampling: non-finite probability");
+        double total = 0.0;
+        for (double t : totals)
+            total += t;
+        if (!(total > 0.0))
+            fail(NUT_ERUNTIME, "sampling: zero probability mass");
+        // the nucleus: the sorted prefix until its mass reaches top_p of the
+        // total (src/generate.cpp:63-68), read in chunks
+        const double cutoff = top_p * total;
+        double nucleus = 0.0;
+        size_t taken = 0;
+        p.clear();
+        ids.clear();
+        do {
+            if (taken == p.size()) {
+                const size_t n = std::min(kChunk, size_t(vocab) - p.size());
+                p.resize(p.size() + n);
+                ids.resize(ids.size() + n);
+                hip_check(hipMemcpy(p.data() + taken, sorted_p + taken, n * sizeof(float),
+                                    hipMemcpyDeviceToHost),
+                          "hipMemcpy to host");
+                hip_check(hipMemcpy(ids.data() + taken, sorted_ids + taken, n * sizeof(int),
+                                    hipMemcpyDeviceToHost),
+                          "hipMemcpy to host");
+            }
+            nucleus += p[taken];
+            taken++;
+        } while (taken < size_t(vocab) && nucleus < cutoff);
+        // the draw and the walk (src/generate.cpp:70-79)
+        std::uniform_real_distribution<double> draw(0.0, nucleus);
+        const double target = draw(rng);
+        double cumulative = 0.0;
+        int token = ids[taken - 1];
+        for (size_t i = 0; i < taken; i++) {
+            cumulative += p[i];
+            if (target <= cumulative) {
+                token = ids[i];
+                break;
+            }
+        }
+        if (size_t(token) == m.config.eos_token)
+            break;
+        out[count++] = token;
+        decode(m, kv, token, nullptr);
+    }
+    const double t2 = now();
     *out_count = count;
     if (stats != nullptr) {
         stats->prefill_tokens = prompt_len;

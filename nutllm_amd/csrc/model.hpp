@@ -78,6 +78,7 @@ struct nut_model {
     // Prefill GEMM path: activations of a whole prompt, max_seq rows each.
     nut::DeviceBuffer pf_h, pf_x, pf_q, pf_k, pf_v, pf_ctx, pf_g, pf_u;
     nut::DeviceBuffer pf_kv; // the batch's K and V as f16 limbs (prefill attention)
+    nut::DeviceBuffer sample_ws; // sampling: numerators, sort buffers
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
     int timeline_wgs = 0;        // workgroups it covers
     unsigned launch_count = 0;
@@ -113,6 +114,12 @@ void logits(nut_model &m, const float *hidden, float *out);
 void generate_greedy(nut_model &m, const int *prompt, size_t prompt_len,
                      size_t max_tokens, int *out, size_t *out_count,
                      nut_generation_stats *stats);
+// generate_tokens_cached with temperature / top-p sampling: device logits,
+// numerators and sort (sample.hip), the reference's sequential nucleus sum
+// and std::mt19937 draw on the host.
+void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
+                      size_t max_tokens, float temperature, float top_p, uint32_t seed,
+                      int *out, size_t *out_count, nut_generation_stats *stats);
 
 bool config_valid(const nut_config &c);
 

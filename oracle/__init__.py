@@ -87,6 +87,8 @@ _REF = {
     "ref_decode_trace": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
     "ref_logits": (C.c_int, [_P, _P, _P, _SZ]),
     "ref_generate": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P]),
+    "ref_generate_sampled": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, C.c_float, C.c_float,
+                                       C.c_uint, _P, _P]),
 }
 
 _orc = None
@@ -327,6 +329,17 @@ class RefModel:
                                  threads, ptr(out), C.byref(count),
                                  C.byref(pre), C.byref(dec)), "ref_generate")
         return out[:count.value].tolist(), pre.value, dec.value
+
+    def generate_sampled(self, prompt, max_tokens, temperature, top_p, seed,
+                         threads=1):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max(1, max_tokens), np.int32)
+        count = C.c_size_t()
+        check(ref().ref_generate_sampled(self.handle, ptr(p), p.size, max_tokens,
+                                         threads, temperature, top_p, seed,
+                                         ptr(out), C.byref(count)),
+              "ref_generate_sampled")
+        return out[:count.value].tolist()
 
     def storage_bytes(self):
         return ref().ref_model_storage_bytes(self.handle)

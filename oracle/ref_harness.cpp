@@ -306,4 +306,24 @@ int ref_generate(void *handle, const int *prompt, size_t n, size_t max_tokens,
     GUARD_END
 }
 
+/* generate_tokens_cached with temperature / top-p sampling. */
+int ref_generate_sampled(void *handle, const int *prompt, size_t n, size_t max_tokens,
+                         size_t threads, float temperature, float top_p, unsigned seed,
+                         int *out, size_t *count)
+{
+    GUARD_BEGIN
+    const QuantizedModelWeights &m = *static_cast<RefModel *>(handle)->weights;
+    SamplingConfig sampling;
+    sampling.max_tokens = max_tokens;
+    sampling.threads = threads;
+    sampling.temperature = temperature;
+    sampling.top_p = top_p;
+    sampling.seed = seed;
+    const std::vector<int> ids = generate_tokens_cached(
+        m, std::vector<int>(prompt, prompt + n), sampling, nullptr);
+    std::memcpy(out, ids.data(), ids.size() * sizeof(int));
+    *count = ids.size();
+    GUARD_END
+}
+
 } // extern "C"

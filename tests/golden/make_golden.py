@@ -21,6 +21,9 @@ Files written:
                   logits, KV cache contents
   tinyllama_int4.json  greedy ids of the TinyLlama-shape INT4 run
                   (5-token prompt, 16 tokens) and its storage_bytes
+  sampled.json    greedy-free runs: generate_tokens_cached with temperature /
+                  top-p / seed (choose_token's sampling branch) on the tiny
+                  INT8 and TinyLlama INT4 models
   tinyllama_int8_2k.npz, llama7b_int4.npz
                   the long-prompt runs (TinyLlama-shape INT8, 2048-token
                   prompt, 128 tokens; Llama-2-7B-shape INT4, 512-token
@@ -224,6 +227,26 @@ def write_tinyllama():
                    "storage_bytes": storage}, f, indent=1)
 
 
+SAMPLING = [(0.7, 0.9, 42), (1.0, 1.0, 7), (0.3, 0.5, 1), (2.0, 0.95, 123)]
+
+
+def write_sampled():
+    """The reference's sampled ids for a few (temperature, top_p, seed)."""
+    runs = []
+    for name, tag in (("tiny_int8", "tiny"), ("tinyllama_int4", "tinyllama")):
+        model, prompt, _ = W.build_run(name)
+        ref = oracle.RefModel.from_quantized(model)
+        for temperature, top_p, seed in SAMPLING:
+            ids = ref.generate_sampled(prompt, 16, temperature, top_p, seed,
+                                       threads=min(8, os.cpu_count() or 1))
+            runs.append({"run": name, "prompt": prompt.tolist(),
+                         "temperature": temperature, "top_p": top_p,
+                         "seed": seed, "ids": ids})
+        ref.close()
+    with open(os.path.join(HERE, "sampled.json"), "w") as f:
+        json.dump(runs, f, indent=1)
+
+
 def kv_sample(c, n):
     """(layer, kv head, position) rows kept from a long run's cache."""
     kvh = c.kv_heads or c.heads
@@ -270,6 +293,9 @@ def copy_fixtures():
 def main():
     if not oracle.ref_available():
         sys.exit("oracle/_ref/libnutref.so is not built: make -C oracle ref")
+    if "--only-sampled" in sys.argv:
+        write_sampled()
+        return
     if "--only-long" in sys.argv:
         for name in ("tinyllama_int8_2k", "llama7b_int4"):
             write_long(name)
@@ -281,6 +307,7 @@ def main():
     copy_fixtures()
     if "--skip-tinyllama" not in sys.argv:
         write_tinyllama()
+        write_sampled()
     if "--long" in sys.argv:
         for name in ("tinyllama_int8_2k", "llama7b_int4"):
             write_long(name)
