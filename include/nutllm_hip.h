@@ -160,6 +160,20 @@ int nut_model_set_layer(nut_model *m, size_t layer, const nut_qmatrix *query,
                         const float *attention_norm, const float *ffn_norm);
 /* QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156). */
 size_t nut_model_storage_bytes(const nut_model *m);
+/* load_llama2c_quantized_model (src/llama2.cpp:339-412) straight into a
+ * device model: the reference's header and size checks and messages
+ * (src/llama2.cpp:199-296, run before the device is touched), pread of one
+ * projection at a time, the product quantiser (bit-exact with
+ * QuantizedMatrix::quantize) on a worker thread overlapping the upload of
+ * the previous layer. A positive vocabulary in the header ties the
+ * classifier to the embeddings; eos_token is 1. *load_seconds (may be
+ * NULL) gets the load's wall time, the reference CLI's load_s
+ * (src/cli.cpp:165-169). */
+int nut_model_load_llama2c(const char *path, int type, nut_model **out,
+                           double *load_seconds);
+/* The configuration, quant type and tied flag a model was created with. */
+int nut_model_config(const nut_model *m, nut_config *config, int *type,
+                     int *tied);
 int nut_model_destroy(nut_model *m);
 
 /* ---------------------------------------------------------- KV cache -- */

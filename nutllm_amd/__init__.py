@@ -127,6 +127,8 @@ _SIGS = {
     "nut_model_timeline": (C.c_int, [_P, _P, _SZ, _P]),
     "nut_model_destroy": (C.c_int, [_P]),
     "nut_token_tag_base": (C.c_int, [_P, _P, _P]),
+    "nut_model_load_llama2c": (C.c_int, [C.c_char_p, C.c_int, _P, _P]),
+    "nut_model_config": (C.c_int, [_P, _P, _P, _P]),
     "nut_model_set_launch_count": (C.c_int, [_P, C.c_uint]),
     "nut_kv_create": (C.c_int, [_P, _P]),
     "nut_kv_destroy": (C.c_int, [_P]),
@@ -445,13 +447,27 @@ class KVCache:
 class DeviceModel:
     """QuantizedModelWeights resident in HBM plus its token loop."""
 
-    def __init__(self, config, qtype, tied=False):
+    def __init__(self, config, qtype, tied=False, _handle=None):
         self.config = config
         self.qtype = qtype
+        if _handle is not None:
+            self.handle = _handle
+            return
         h = C.c_void_p()
         check(lib().nut_model_create(C.byref(config), qtype, int(tied),
                                      C.byref(h)))
         self.handle = h
+
+    @classmethod
+    def load_llama2c(cls, path, qtype):
+        """load_llama2c_quantized_model into HBM: (model, load seconds)."""
+        h = C.c_void_p()
+        seconds = C.c_double()
+        check(lib().nut_model_load_llama2c(os.fsencode(path), qtype,
+                                           C.byref(h), C.byref(seconds)))
+        cfg = Config()
+        check(lib().nut_model_config(h, C.byref(cfg), None, None))
+        return cls(cfg, qtype, _handle=h), seconds.value
 
     def set_globals(self, embeddings, final_norm, lm_head=None):
         e = np.ascontiguousarray(embeddings, np.float32)

@@ -338,6 +338,29 @@ int nut_model_set_launch_count(nut_model *m, unsigned launch_count)
     });
 }
 
+int nut_model_load_llama2c(const char *path, int type, nut_model **out,
+                           double *load_seconds)
+{
+    return nut::guarded([&]() {
+        nut::require(out != nullptr, NUT_EINVAL, "llama2 checkpoint: null output");
+        *out = nullptr;
+        *out = nut::load_llama2c(path, type, load_seconds);
+    });
+}
+
+int nut_model_config(const nut_model *m, nut_config *config, int *type, int *tied)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && config != nullptr, NUT_EINVAL,
+                     "quantized model: null pointer");
+        *config = m->config;
+        if (type != nullptr)
+            *type = m->type;
+        if (tied != nullptr)
+            *tied = m->tied ? 1 : 0;
+    });
+}
+
 size_t nut_model_storage_bytes(const nut_model *m)
 {
     return m == nullptr ? 0 : nut::storage_bytes(*m);

@@ -123,4 +123,8 @@ void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
 
 bool config_valid(const nut_config &c);
 
+// load_llama2c_quantized_model (src/llama2.cpp:339-412) into a device model;
+// *seconds gets the wall time of the whole load (may be null).
+nut_model *load_llama2c(const char *path, int type, double *seconds);
+
 } // namespace nut

@@ -49,3 +49,24 @@ def load(path):
                   ffn_dim=ffn, vocab_size=vocab, max_seq=max_seq,
                   eos_token=1, kv_heads=kv_heads)
     return config, w, shared
+
+
+def write(path, config, w, shared=False):
+    """Write a llama2.c checkpoint (the layout load() reads) from a config
+    dict and a weights dict keyed as load() returns them; the RoPE tables
+    are written as zeros (the loaders skip them)."""
+    c = config
+    head_dim = c["dim"] // c["heads"]
+    vocab = c["vocab_size"] if shared else -c["vocab_size"]
+    header = np.array([c["dim"], c["ffn_dim"], c["layers"], c["heads"],
+                       c["kv_heads"], vocab, c["max_seq"]], np.int32)
+    parts = [w["embeddings"], w["attention_norm"], w["query"], w["key"],
+             w["value"], w["output"], w["ffn_norm"], w["gate"], w["down"],
+             w["up"], w["final_norm"],
+             np.zeros((c["max_seq"], head_dim), np.float32)]
+    if not shared:
+        parts.append(w["classifier"])
+    with open(path, "wb") as f:
+        f.write(header.tobytes())
+        for p in parts:
+            f.write(np.ascontiguousarray(p, np.float32).tobytes())
