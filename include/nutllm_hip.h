@@ -253,6 +253,34 @@ int nut_generate_sampled(nut_model *m, const int *prompt, size_t prompt_len,
                          uint32_t seed, int *out, size_t *out_count,
                          nut_generation_stats *stats);
 
+/* ---------------------------------------------------- fp32 model path -- */
+
+/* ModelWeights (include/loader.hpp:46-60) in HBM: fp32 embeddings
+ * [vocab x dim], final_norm [dim], lm_head [vocab x dim] (ignored when
+ * tied), and per layer the projections in the reference's [in x out]
+ * layout (LayerWeights, src/attention.cpp:29-40): query dim x dim, key and
+ * value dim x kv_dim, output dim x dim, gate and up dim x ffn, down
+ * ffn x dim. The KV cache is the same nut_kvcache. */
+typedef struct nut_fmodel nut_fmodel;
+int nut_fmodel_create(const nut_config *config, int tied, nut_fmodel **out);
+int nut_fmodel_set_globals(nut_fmodel *m, const float *embeddings,
+                           const float *final_norm, const float *lm_head);
+int nut_fmodel_set_layer(nut_fmodel *m, size_t layer, const float *query,
+                         const float *key, const float *value,
+                         const float *output, const float *gate,
+                         const float *up, const float *down,
+                         const float *attention_norm, const float *ffn_norm);
+int nut_fmodel_destroy(nut_fmodel *m);
+/* decode_token (src/kvcache.cpp:264-284): one token at position = length;
+ * hidden (host, may be NULL) gets the hidden state after the last layer. */
+int nut_decode_token(nut_fmodel *m, nut_kvcache *kv, int token,
+                     float *hidden);
+/* prefill_tokens (src/kvcache.cpp:237-262): resets the cache and runs the
+ * tokens; rows (host, may be NULL) gets every token's hidden state,
+ * [count x dim]. */
+int nut_prefill_tokens(nut_fmodel *m, nut_kvcache *kv, const int *tokens,
+                       size_t count, float *rows);
+
 /* Execution path of decode / prefill / generate (no reference counterpart;
  * every path computes the same function): NUT_PATH_AUTO picks the
  * cooperative token kernel when the shape has an instantiation and the

@@ -145,6 +145,12 @@ _SIGS = {
     "nut_prefill": (C.c_int, [_P, _P, _P, _SZ, _P]),
     "nut_logits": (C.c_int, [_P, _P, _P]),
     "nut_generate_greedy": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
+    "nut_fmodel_create": (C.c_int, [_P, C.c_int, _P]),
+    "nut_fmodel_set_globals": (C.c_int, [_P, _P, _P, _P]),
+    "nut_fmodel_set_layer": (C.c_int, [_P, _SZ] + [_P] * 9),
+    "nut_fmodel_destroy": (C.c_int, [_P]),
+    "nut_decode_token": (C.c_int, [_P, _P, C.c_int, _P]),
+    "nut_prefill_tokens": (C.c_int, [_P, _P, _P, _SZ, _P]),
     "nut_generate_sampled": (C.c_int, [_P, _P, _SZ, _SZ, C.c_float, C.c_float,
                                        C.c_uint32, _P, _P, _P]),
     "nut_kv_read_positions": (C.c_int, [_P, _SZ, _SZ, _P, _P]),
@@ -579,6 +585,55 @@ class DeviceModel:
     def close(self):
         if self.handle:
             check(lib().nut_model_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceFModel:
+    """fp32 ModelWeights resident in HBM: decode_token / prefill_tokens
+    (src/kvcache.cpp:237-284). Projections in the reference's [in x out]
+    layout."""
+
+    def __init__(self, config, tied=False):
+        self.config = config
+        self.tied = tied
+        h = C.c_void_p()
+        check(lib().nut_fmodel_create(C.byref(config), int(tied), C.byref(h)))
+        self.handle = h
+
+    def set_globals(self, embeddings, final_norm, lm_head=None):
+        e = np.ascontiguousarray(embeddings, np.float32)
+        n = np.ascontiguousarray(final_norm, np.float32)
+        l = None if lm_head is None else np.ascontiguousarray(lm_head, np.float32)
+        check(lib().nut_fmodel_set_globals(self.handle, _ptr(e), _ptr(n), _ptr(l)))
+
+    def set_layer(self, index, weights, attention_norm, ffn_norm):
+        ws = [np.ascontiguousarray(weights[n], np.float32) for n in PROJECTIONS]
+        an = np.ascontiguousarray(attention_norm, np.float32)
+        fn = np.ascontiguousarray(ffn_norm, np.float32)
+        check(lib().nut_fmodel_set_layer(self.handle, index, *[_ptr(w) for w in ws],
+                                         _ptr(an), _ptr(fn)))
+
+    def decode(self, cache, token):
+        hidden = np.empty(self.config.dim, np.float32)
+        check(lib().nut_decode_token(self.handle, cache.handle, int(token), _ptr(hidden)))
+        return hidden
+
+    def prefill(self, cache, tokens):
+        t = np.ascontiguousarray(tokens, np.int32)
+        rows = np.empty((t.size, self.config.dim), np.float32)
+        check(lib().nut_prefill_tokens(self.handle, cache.handle, _ptr(t), t.size,
+                                       _ptr(rows)))
+        return rows
+
+    def close(self):
+        if self.handle:
+            check(lib().nut_fmodel_destroy(self.handle))
             self.handle = None
 
     def __del__(self):

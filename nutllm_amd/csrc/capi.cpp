@@ -4,6 +4,7 @@
 #include <cstring>
 #include <unordered_map>
 
+#include "fmodel.hpp"
 #include "kernels.hpp"
 #include "model.hpp"
 #include "persistent.hpp"
@@ -531,6 +532,63 @@ int nut_generate_sampled(nut_model *m, const int *prompt, size_t prompt_len,
         nut::ensure_device();
         nut::generate_sampled(*m, prompt, prompt_len, max_tokens, temperature, top_p, seed, out,
                               out_count, stats);
+    });
+}
+
+int nut_fmodel_create(const nut_config *config, int tied, nut_fmodel **out)
+{
+    return nut::guarded([&]() {
+        nut::require(config != nullptr && out != nullptr, NUT_EINVAL,
+                     "fp32 model: null pointer");
+        *out = nullptr;
+        *out = nut::create_fmodel(*config, tied != 0);
+    });
+}
+
+int nut_fmodel_set_globals(nut_fmodel *m, const float *embeddings, const float *final_norm,
+                           const float *lm_head)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "fp32 model: null model");
+        nut::ensure_device();
+        nut::set_fglobals(*m, embeddings, final_norm, lm_head);
+    });
+}
+
+int nut_fmodel_set_layer(nut_fmodel *m, size_t layer, const float *query, const float *key,
+                         const float *value, const float *output, const float *gate,
+                         const float *up, const float *down, const float *attention_norm,
+                         const float *ffn_norm)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "fp32 model: null model");
+        nut::ensure_device();
+        const float *const w[7] = {query, key, value, output, gate, up, down};
+        nut::set_flayer(*m, layer, w, attention_norm, ffn_norm);
+    });
+}
+
+int nut_fmodel_destroy(nut_fmodel *m)
+{
+    return nut::guarded([&]() { delete m; });
+}
+
+int nut_decode_token(nut_fmodel *m, nut_kvcache *kv, int token, float *hidden)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && kv != nullptr, NUT_EINVAL, "kv cache: null pointer");
+        nut::ensure_device();
+        nut::decode_token(*m, *kv, token, hidden);
+    });
+}
+
+int nut_prefill_tokens(nut_fmodel *m, nut_kvcache *kv, const int *tokens, size_t count,
+                       float *rows)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr && kv != nullptr, NUT_EINVAL, "kv cache: null pointer");
+        nut::ensure_device();
+        nut::prefill_tokens(*m, *kv, tokens, count, rows);
     });
 }
 

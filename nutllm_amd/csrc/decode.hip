@@ -399,6 +399,17 @@ void launch_embed(const DecodeShape &s, const float *embeddings,
     check_launch("decode: embedding");
 }
 
+void launch_attention(const DecodeShape &s, const float *query, const float *k_layer,
+                      const float *v_layer, const int *length, float *context,
+                      const StepState *state, hipStream_t stream)
+{
+    const size_t attn_lds =
+        sizeof(float) * (size_t(s.head_dim) + kThreads + kWaves + s.max_seq);
+    hipLaunchKernelGGL(attention_kernel, dim3(s.heads), dim3(kThreads), attn_lds, stream, s,
+                       query, k_layer, v_layer, length, context, state);
+    check_launch("decode: attention");
+}
+
 void launch_layer(const DecodeShape &s, const LayerView &w,
                   const float2 *rope, const int *length, float *k_layer,
                   float *v_layer, float *hidden, float *query, float *context,

@@ -80,6 +80,12 @@ void launch_layer(const DecodeShape &s, const LayerView &w,
                   float *act, const StepState *state, hipStream_t stream);
 void launch_finish_step(const StepState *state, int *length,
                         hipStream_t stream);
+// GQA attention of one decode step (attention_step's softmax and context,
+// src/quant_model.cpp:68-105): query [heads][head_dim] at position *length
+// over cached positions 0..*length, context [heads][head_dim].
+void launch_attention(const DecodeShape &s, const float *query, const float *k_layer,
+                      const float *v_layer, const int *length, float *context,
+                      const StepState *state, hipStream_t stream);
 // Final rmsnorm + fp32 classifier; logits may be null. Writes per-block
 // argmax partials (value, index) for launch_pick_token.
 int classifier_blocks(const DecodeShape &s);

@@ -43,6 +43,10 @@ DecodeShape shape_of(const nut_config &c)
     return s;
 }
 
+void upload(void *dst, const void *src, size_t bytes);
+
+} // namespace
+
 // cos/sin of rotate_vector (src/quant_model.cpp:26-37), computed exactly as
 // the reference does: double frequency 10000^(-pair/hd), double angle,
 // rounded to fp32. Entry [pos][pair/2] = (cos, sin).
@@ -60,6 +64,8 @@ std::vector<float> rope_table(const nut_config &c)
         }
     return table;
 }
+
+namespace {
 
 void upload(void *dst, const void *src, size_t bytes)
 {

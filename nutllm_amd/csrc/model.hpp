@@ -123,6 +123,10 @@ void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
 
 bool config_valid(const nut_config &c);
 
+// RoPE cos/sin table [max_seq][head_dim / 2] of (cos, sin) as fp32, from the
+// reference's double-precision formula (src/quant_model.cpp:26-37).
+std::vector<float> rope_table(const nut_config &c);
+
 // load_llama2c_quantized_model (src/llama2.cpp:339-412) into a device model;
 // *seconds gets the wall time of the whole load (may be null).
 nut_model *load_llama2c(const char *path, int type, double *seconds);

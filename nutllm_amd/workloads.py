@@ -171,3 +171,58 @@ def build_run(name, keep_fp32=False):
     model = build(shape, qtype, seed, max_seq, keep_fp32)
     prompt = synth_tokens(prompt_seed, model.config.vocab_size, prompt_len)
     return model, prompt, gen
+
+
+# fp32 model path (ModelWeights, decode_token / prefill_tokens): the same
+# streams as the quantised models, each projection drawn as its reference
+# [in x out] Matrix.
+FP32_SHAPES = {"query": lambda c: (c.dim, c.dim), "key": lambda c: (c.dim, c.kv_dim),
+               "value": lambda c: (c.dim, c.kv_dim), "output": lambda c: (c.dim, c.dim),
+               "gate": lambda c: (c.dim, c.ffn_dim), "up": lambda c: (c.dim, c.ffn_dim),
+               "down": lambda c: (c.ffn_dim, c.dim)}
+
+
+@dataclass
+class SynthFModel:
+    """Host copy of a synthetic fp32 ModelWeights ([in x out] projections)."""
+
+    config: Config
+    seed: int
+    tied: bool
+    embeddings: np.ndarray
+    final_norm: np.ndarray
+    lm_head: np.ndarray
+    layers: list
+    norms: list
+
+    def to_device(self):
+        from . import DeviceFModel
+        m = DeviceFModel(self.config, self.tied)
+        m.set_globals(self.embeddings, self.final_norm,
+                      None if self.tied else self.lm_head)
+        for i, w in enumerate(self.layers):
+            m.set_layer(i, w, *self.norms[i])
+        return m
+
+
+def build_fp32(shape, seed, max_seq=None, norm_seed=None, tied=False):
+    cfg = make_config(shape, max_seq)
+    n = cfg.vocab_size * cfg.dim
+    emb = synth_normal(seed, STREAM_EMBED, n, SIGMA).reshape(cfg.vocab_size, cfg.dim)
+    head = emb if tied else synth_normal(seed, STREAM_CLASSIFIER, n, SIGMA).reshape(
+        cfg.vocab_size, cfg.dim)
+    layers = []
+    for layer in range(cfg.layers):
+        w = {}
+        for name in PROJECTIONS:
+            rows, cols = FP32_SHAPES[name](cfg)
+            w[name] = synth_normal(seed, stream_of(layer, name), rows * cols,
+                                   SIGMA).reshape(rows, cols)
+        layers.append(w)
+    if norm_seed is None:
+        ones = np.ones(cfg.dim, np.float32)
+        norms, final = [(ones, ones)] * cfg.layers, ones
+    else:
+        norms, final = seeded_norms(norm_seed, cfg.dim, cfg.layers)
+    return SynthFModel(cfg, seed, tied, emb, final, head, layers, norms)
+

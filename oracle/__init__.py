@@ -87,6 +87,10 @@ _REF = {
     "ref_decode_trace": (C.c_int, [_P, _P, _SZ, _SZ, _P, _P, _P]),
     "ref_logits": (C.c_int, [_P, _P, _P, _SZ]),
     "ref_generate": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, _P, _P, _P, _P]),
+    "ref_fmodel_create": (C.c_int, [_P, C.c_int, _P, _P, _P, _P]),
+    "ref_fmodel_add_layer": (C.c_int, [_P] * 10),
+    "ref_fmodel_free": (None, [_P]),
+    "ref_fmodel_run": (C.c_int, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _P, _P, _P]),
     "ref_generate_sampled": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, C.c_float, C.c_float,
                                        C.c_uint, _P, _P]),
 }

@@ -24,6 +24,7 @@
 #undef private
 #include "generate.hpp"
 #include "kvcache.hpp"
+#include "loader.hpp"
 #include "matmul.hpp"
 #include "ops.hpp"
 #include "quant_model.hpp"
@@ -323,6 +324,81 @@ int ref_generate_sampled(void *handle, const int *prompt, size_t n, size_t max_t
         m, std::vector<int>(prompt, prompt + n), sampling, nullptr);
     std::memcpy(out, ids.data(), ids.size() * sizeof(int));
     *count = ids.size();
+    GUARD_END
+}
+
+/* ------------------------------------------------ fp32 model path --- */
+
+struct RefFModel {
+    std::unique_ptr<ModelWeights> weights;
+    size_t filled = 0; // layers set so far (the constructor makes them all)
+};
+
+/* ModelWeights with fp32 embeddings, final norm and (unless tied) lm_head;
+ * layers appended by ref_fmodel_add_layer. */
+int ref_fmodel_create(const size_t *config, int tied, const float *embeddings,
+                      const float *final_norm, const float *lm_head, void **out)
+{
+    GUARD_BEGIN
+    const ModelConfig c = config_of(config);
+    auto model = std::make_unique<RefFModel>();
+    model->weights = std::make_unique<ModelWeights>(c, tied == 0);
+    ModelWeights &m = *model->weights;
+    m.tied_embeddings = tied != 0;
+    std::memcpy(m.embeddings.data(), embeddings, c.vocab_size * c.dim * sizeof(float));
+    m.final_norm.assign(final_norm, final_norm + c.dim);
+    if (!tied)
+        std::memcpy(m.lm_head.data(), lm_head, c.vocab_size * c.dim * sizeof(float));
+    *out = model.release();
+    GUARD_END
+}
+
+/* The next layer's [in x out] fp32 projections (LayerWeights). */
+int ref_fmodel_add_layer(void *handle, const float *query, const float *key,
+                         const float *value, const float *output, const float *gate,
+                         const float *up, const float *down, const float *attention_norm,
+                         const float *ffn_norm)
+{
+    GUARD_BEGIN
+    RefFModel &r = *static_cast<RefFModel *>(handle);
+    ModelWeights &m = *r.weights;
+    if (r.filled >= m.layers.size())
+        throw std::out_of_range("harness: too many layers");
+    LayerWeights &l = m.layers[r.filled++];
+    const float *src[7] = {query, key, value, output, gate, up, down};
+    Matrix *dst[7] = {&l.query, &l.key, &l.value, &l.output, &l.gate, &l.up, &l.down};
+    for (int i = 0; i < 7; i++)
+        std::memcpy(dst[i]->data(), src[i], dst[i]->size() * sizeof(float));
+    l.attention_norm.assign(attention_norm, attention_norm + m.config.dim);
+    l.ffn_norm.assign(ffn_norm, ffn_norm + m.config.dim);
+    GUARD_END
+}
+
+void ref_fmodel_free(void *handle) { delete static_cast<RefFModel *>(handle); }
+
+/* prefill_tokens over the prompt (every row of its output), then
+ * decode_token for each of `tokens` (each hidden state), then the cache. */
+int ref_fmodel_run(void *handle, const int *prompt, size_t n, const int *tokens, size_t m,
+                   size_t threads, float *rows, float *hidden, float *keys, float *values)
+{
+    GUARD_BEGIN
+    const ModelWeights &w = *static_cast<RefFModel *>(handle)->weights;
+    const ModelConfig &c = w.config;
+    KVCache cache(c);
+    const Matrix out = prefill_tokens(w, std::vector<int>(prompt, prompt + n), cache, threads);
+    std::memcpy(rows, out.data(), n * c.dim * sizeof(float));
+    for (size_t t = 0; t < m; t++) {
+        const std::vector<float> h = decode_token(w, tokens[t], cache, threads);
+        std::memcpy(hidden + t * c.dim, h.data(), c.dim * sizeof(float));
+    }
+    const size_t kv = c.effective_kv_heads(), hd = c.head_dim;
+    for (size_t l = 0; l < c.layers; l++)
+        for (size_t h = 0; h < kv; h++)
+            for (size_t p = 0; p < cache.length(); p++) {
+                const size_t o = ((l * kv + h) * c.max_seq + p) * hd;
+                std::memcpy(keys + o, cache.key(l, h, p), hd * sizeof(float));
+                std::memcpy(values + o, cache.value(l, h, p), hd * sizeof(float));
+            }
     GUARD_END
 }
 

@@ -21,6 +21,10 @@ Files written:
                   logits, KV cache contents
   tinyllama_int4.json  greedy ids of the TinyLlama-shape INT4 run
                   (5-token prompt, 16 tokens) and its storage_bytes
+  fp32_*.npz      the fp32 model path (ModelWeights): prefill_tokens rows
+                  for a 6-token prompt, then 4 decode_token hidden states
+                  and the KV cache, for the tiny shape (untied and tied)
+                  and a dim-256 / head_dim-64 shape
   sampled.json    greedy-free runs: generate_tokens_cached with temperature /
                   top-p / seed (choose_token's sampling branch) on the tiny
                   INT8 and TinyLlama INT4 models
@@ -247,6 +251,39 @@ def write_sampled():
         json.dump(runs, f, indent=1)
 
 
+FP32_RUNS = [("tiny", 21, False), ("tiny", 23, True), ("step_gqa2", 22, False)]
+
+
+def write_fp32():
+    for shape, seed, tied in FP32_RUNS:
+        model = W.build_fp32(shape, seed, max_seq=64, norm_seed=seed + 100, tied=tied)
+        c = model.config
+        cfg = (oracle.C.c_size_t * 9)(*[getattr(c, n) for n, _ in oracle.OrcConfig._fields_])
+        h = oracle.C.c_void_p()
+        oracle.check(oracle.ref().ref_fmodel_create(
+            cfg, int(tied), oracle.ptr(model.embeddings), oracle.ptr(model.final_norm),
+            None if tied else oracle.ptr(model.lm_head), oracle.C.byref(h)))
+        for i, w in enumerate(model.layers):
+            oracle.check(oracle.ref().ref_fmodel_add_layer(
+                h, *[oracle.ptr(np.ascontiguousarray(w[n])) for n in oracle.PROJECTIONS],
+                oracle.ptr(model.norms[i][0]), oracle.ptr(model.norms[i][1])))
+        prompt = W.synth_tokens(seed, c.vocab_size, 6)
+        tokens = W.synth_tokens(seed + 1, c.vocab_size, 4)
+        kv = oracle.orc().orc_kv_elements(oracle.C.byref(oracle.OrcConfig(
+            **{n: getattr(c, n) for n, _ in oracle.OrcConfig._fields_})))
+        rows = np.zeros((6, c.dim), np.float32)
+        hidden = np.zeros((4, c.dim), np.float32)
+        keys, values = np.zeros(kv, np.float32), np.zeros(kv, np.float32)
+        oracle.check(oracle.ref().ref_fmodel_run(
+            h, oracle.ptr(prompt), 6, oracle.ptr(tokens), 4, 1, oracle.ptr(rows),
+            oracle.ptr(hidden), oracle.ptr(keys), oracle.ptr(values)), "ref_fmodel_run")
+        oracle.ref().ref_fmodel_free(h)
+        tag = f"fp32_{shape}{'_tied' if tied else ''}"
+        np.savez_compressed(os.path.join(HERE, f"{tag}.npz"), prompt=prompt, tokens=tokens,
+                            rows=rows, hidden=hidden, keys=keys, values=values,
+                            seed=np.int64(seed), tied=np.int64(tied))
+
+
 def kv_sample(c, n):
     """(layer, kv head, position) rows kept from a long run's cache."""
     kvh = c.kv_heads or c.heads
@@ -296,6 +333,9 @@ def main():
     if "--only-sampled" in sys.argv:
         write_sampled()
         return
+    if "--only-fp32" in sys.argv:
+        write_fp32()
+        return
     if "--only-long" in sys.argv:
         for name in ("tinyllama_int8_2k", "llama7b_int4"):
             write_long(name)
@@ -305,6 +345,7 @@ def main():
     write_tiny(INT8, "int8")
     write_tiny(INT4, "int4")
     copy_fixtures()
+    write_fp32()
     if "--skip-tinyllama" not in sys.argv:
         write_tinyllama()
         write_sampled()
