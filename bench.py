@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
-"""bench.py — decode throughput of the gfx950 token loop on one MI355X.
+"""bench.py — throughput of the gfx950 token loop on one MI355X.
 
-Workload (a "step"): one greedy generate_tokens_cached call
+Default workload (a "step"): one greedy generate_tokens_cached call
 (src/generate.cpp:174-216) on the TinyLlama-1.1B-shaped decoder with random
 N(0, 0.02) weights (seed 3), INT4 block-32 linears, fp32 embeddings and
 classifier: a 5-token prompt, then 16 greedy tokens. Weights and KV cache are
@@ -15,14 +15,31 @@ roofline  algorithmic bytes of the decode loop (packed weights + fp16 scales
           model's stream, against the 8 TB/s HBM peak.
 cpu_baseline  the compiled reference's own threaded generate_tokens_cached
           (oracle/_ref, "reference") or, when that library is absent, this
-          repo's C restatement ("port"), timed on this host in the same run.
+          repo's C restatement ("port"), timed on this host in the same run
+          at 1, 4 and the host's physical cores (at most 16, the box's CPU
+          share); value is the physical-core figure.
 
-One JSON line goes to stdout; progress to stderr.
+Other workloads (--workload), one JSON line each:
+  tinyllama_int8_2k, llama7b_int4
+          2048- / 512-token prompt (batched MFMA prefill) then 128 greedy
+          tokens: decode tok/s with its HBM roofline (weights + K/V at each
+          step's context), prefill tok/s with its MFMA roofline, the
+          reference CPU decode loop timed on a bounded sample at the same
+          context, and whether the ids equal the reference's
+          (tests/golden/<workload>.npz).
+  kernels the standalone quantised matvec (5 shapes x INT4/INT8, weights
+          rotated past the 256 MB memory-side cache) and the 768^3 fp32
+          GEMM, from nutllm_amd/lib/nut_kernel_bench (launches issued from
+          C++), each with the reference's matvec_quantized_threaded /
+          matmul_threaded timed beside it; one line per kernel and shape.
+
+Progress goes to stderr.
 """
 import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -30,17 +47,46 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16, MI355X
 PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 
 # HBM bytes one generate launch (16 iterations) moves, from rocprofv3
-# counter runs of this bench: FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB (the
-# scales read off a 1 GiB device-to-device copy in the same runs).
+# counter runs of this bench (profiles/token_kernel_tinyllama_int4_decode.md):
+# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB, the scales read off a 1 GiB
+# device-to-device copy in the same runs.
 MEASURED_TRAFFIC_BYTES = 13_535_426_731
-CPU_SAMPLE_SECONDS = 10.0
+CPU_SAMPLE_SECONDS = 8.0
+MAX_THREADS = 16  # the GPU box's CPU share
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_info():
+    """CPU model name and physical core count of this host."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                key, value = key.strip(), value.strip()
+                if key == "model name":
+                    model = value
+                elif key == "physical id":
+                    phys = value
+                elif key == "core id":
+                    core = value
+                elif not key and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:
+        pass
+    if phys is not None and core is not None:
+        cores.add((phys, core))
+    n = len(cores) or (os.cpu_count() or 1)
+    return model, n
 
 
 def kv_bytes_per_position(cfg):
@@ -48,42 +94,60 @@ def kv_bytes_per_position(cfg):
     return 2 * cfg.layers * kv * cfg.head_dim * 4
 
 
+def thread_counts():
+    model, physical = cpu_info()
+    top = max(1, min(physical, MAX_THREADS, os.cpu_count() or 1))
+    return model, physical, sorted({1, min(4, top), top})
+
+
 def cpu_baseline(model, prompt, gen):
+    """The reference's generate_tokens_cached at 1, 4 and all physical
+    cores (each for about CPU_SAMPLE_SECONDS)."""
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    cpu_model, physical, counts = thread_counts()
     if oracle.ref_available():
         kind = "reference"
         rm = oracle.RefModel.from_quantized(model)
-        run = lambda: rm.generate(prompt, gen, threads)  # noqa: E731
+        run = lambda t: rm.generate(prompt, gen, t)  # noqa: E731
     else:
         kind = "port"
-        oracle.orc().orc_set_threads(threads)
         om = oracle.oracle_model(model)
-        run = lambda: om.generate(prompt, gen)  # noqa: E731
-    rates, prefill = [], []
-    ids = None
-    start = time.perf_counter()
-    # repeat whole generate calls for about CPU_SAMPLE_SECONDS (at most 30)
-    while len(rates) < 30 and (len(rates) < 2 or time.perf_counter() - start
-                               < CPU_SAMPLE_SECONDS):
-        ids, pre, dec = run()
-        rates.append(len(ids) / dec)
-        prefill.append(len(prompt) / pre)
-    elapsed = time.perf_counter() - start
+
+        def run(t):
+            oracle.orc().orc_set_threads(t)
+            return om.generate(prompt, gen)
+    by_threads, prefill, ids, total = {}, {}, None, 0.0
+    for t in counts:
+        rates, pre = [], []
+        start = time.perf_counter()
+        while len(rates) < 30 and (len(rates) < 2 or time.perf_counter() - start
+                                   < CPU_SAMPLE_SECONDS):
+            ids, p, d = run(t)
+            rates.append(len(ids) / d)
+            pre.append(len(prompt) / p)
+        total += time.perf_counter() - start
+        by_threads[str(t)] = round(statistics.median(rates), 3)
+        prefill[str(t)] = round(statistics.median(pre), 3)
+    top = str(counts[-1])
     return {
-        "value": round(statistics.median(rates), 3),
+        "value": by_threads[top],
         "unit": "tok/s",
-        "cores": threads,
+        "cores": counts[-1],
         "kind": kind,
-        "sample": (f"TinyLlama-shape INT4 greedy generate, {len(prompt)}-token "
-                   f"prompt + {gen} tokens, median of {len(rates)} runs "
-                   f"({elapsed:.1f} s), {threads} threads; prefill "
-                   f"{statistics.median(prefill):.3f} tok/s"),
+        "cpu_model": cpu_model,
+        "physical_cores": physical,
+        "by_threads": by_threads,
+        "prefill_tok_s_by_threads": prefill,
+        "sample": (f"TinyLlama-shape INT4 greedy generate_tokens_cached, "
+                   f"{len(prompt)}-token prompt + {gen} tokens, median of up to 30 "
+                   f"runs per thread count ({total:.1f} s in all), GenerationStats "
+                   f"semantics; value at {top} threads"),
     }, ids
 
 
 def long_prompt(args, nut, workloads):
-    """Prefill (batched GEMM path) and decode tok/s of a long-prompt run."""
+    """Prefill (batched GEMM path) and decode of a long-prompt run."""
+    import numpy as np
     t = time.time()
     model, prompt, gen = workloads.build_run(args.workload)
     log(f"built synthetic model in {time.time() - t:.1f}s")
@@ -115,37 +179,138 @@ def long_prompt(args, nut, workloads):
     for _ in range(args.warmup):
         dev.generate(prompt, gen)
     pre, dec, toks, dms = [], [], 0, []
+    t0 = time.perf_counter()
     for _ in range(args.steps):
         ids, st = dev.generate(prompt, gen)
         pre.append(st.prefill_seconds)
         dec.append(st.decode_seconds)
         dms.append(dev.last_decode_ms())
         toks += st.generated_tokens
+    t1 = time.perf_counter()
     dev.close()
     n = len(ids)
     # the greedy ids the reference generated for this run (tests/golden)
     golden = os.path.join(ROOT, "tests", "golden", f"{args.workload}.npz")
-    ref_ids = None
-    if os.path.exists(golden):
-        import numpy as np
-        ref_ids = np.load(golden)["ids"].tolist()
+    ref_ids = np.load(golden)["ids"].tolist() if os.path.exists(golden) else None
     prefill_s = statistics.median(pre)
     linear = sum(2 * r * c for r, c in nut.projection_shapes(cfg).values())
-    kv = cfg.kv_heads or cfg.heads
     attn = sum(4 * cfg.heads * cfg.head_dim * (i + 1) for i in range(len(prompt)))
     flop = len(prompt) * linear * cfg.layers + attn * cfg.layers
-    print(json.dumps({
-        "workload": args.workload, "prompt_tokens": len(prompt),
-        "generated_tokens": n, "steps": args.steps, "warmup": args.warmup,
+    device_ms = statistics.median(dms)
+    per_pos = kv_bytes_per_position(cfg)
+    kv_bytes = sum(per_pos * (len(prompt) + i + 1) for i in range(n))
+    step_bytes = model.weight_bytes_per_token() * n + kv_bytes
+    achieved = step_bytes / (device_ms * 1e-3) / 1e9
+    line = {
+        "metric": f"decode tok/s, {args.workload} (greedy, {len(prompt)}-token prompt, "
+                  f"{gen} tokens)",
+        "value": round(toks / sum(dec), 2),
+        "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round((t1 - t0) * 1e3 / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if model.qtype == 0 else "int4",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        "config": {"workload": args.workload, "dim": cfg.dim, "layers": cfg.layers,
+                   "heads": cfg.heads, "kv_heads": cfg.kv_heads or cfg.heads,
+                   "ffn_dim": cfg.ffn_dim, "vocab": cfg.vocab_size,
+                   "prompt_tokens": len(prompt), "generated_tokens": n},
+        "decode_device_us_per_token": round(device_ms * 1e3 / n, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "decode loop (classifier + argmax + "
+                     "decode step per token)", "bytes_per_launch": step_bytes},
         "prefill_tok_s": round(len(prompt) / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
-        "prefill_tflops": round(flop / prefill_s / 1e12, 2),
-        "decode_tok_s": round(toks / sum(dec), 2),
-        "decode_device_us_per_token": round(statistics.median(dms) * 1e3 / n, 1),
-        "kv_heads": kv, "dtype": "fp32",
-        "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
+        "prefill_roofline": {"bound": "mfma", "achieved": round(flop / prefill_s / 1e12, 1),
+                             "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(flop / prefill_s / 1e12 / F16_MFMA_PEAK_TFLOPS, 4),
+                             "flop": flop},
         "ids_match_reference": None if ref_ids is None else ids == ref_ids,
-    }), flush=True)
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = long_cpu_baseline(model, prompt, ids)
+    print(json.dumps(line), flush=True)
+
+
+def long_cpu_baseline(model, prompt, ids):
+    """The reference's decode loop (norm, classifier, argmax,
+    decode_quantized_token) from the workload's context, on a bounded
+    sample; and the same from the prompt's mean position (the reference
+    prefills token by token, so that is its prefill rate there)."""
+    import oracle
+    if not oracle.ref_available():
+        return None
+    cpu_model, physical, counts = thread_counts()
+    threads = counts[-1]
+    rm = oracle.RefModel.from_quantized(model)
+    toks = list(ids) + [int(t) for t in prompt]
+    room = model.config.max_seq - len(prompt)  # the cache holds max_seq rows
+    one = rm.decode_time(len(prompt), toks[:1], threads)
+    k = max(1, min(len(toks), room, int(15.0 / max(one, 1e-3))))
+    dec_s = rm.decode_time(len(prompt), toks[:k], threads)
+    mid = len(prompt) // 2
+    kp = max(1, min(len(toks), k, model.config.max_seq - mid))
+    pre_s = rm.decode_time(mid, toks[:kp], threads)
+    rm.close()
+    return {
+        "value": round(k / dec_s, 3), "unit": "tok/s", "cores": threads,
+        "kind": "reference", "cpu_model": cpu_model, "physical_cores": physical,
+        "prefill_tok_s": round(kp / pre_s, 3),
+        "sample": (f"{k} decode-loop steps of the reference (final rmsnorm, fp32 "
+                   f"classifier, argmax, decode_quantized_token) from context "
+                   f"{len(prompt)} ({dec_s:.1f} s); prefill rate: {kp} steps from "
+                   f"position {mid}, the prompt's mean position ({pre_s:.1f} s); "
+                   f"{threads} threads"),
+    }
+
+
+def kernels(args):
+    """Standalone kernels (nut_kernel_bench) with the reference beside them."""
+    import numpy as np
+
+    import nutllm_amd as nut
+    binary = os.path.join(ROOT, "nutllm_amd", "lib", "nut_kernel_bench")
+    out = subprocess.run([binary, "--iters", str(max(20, args.steps * 40))],
+                         capture_output=True, text=True, check=True).stdout
+    lines = [json.loads(x) for x in out.splitlines() if x.startswith("{")]
+    ref = None
+    if not args.no_cpu:
+        import oracle
+        ref = oracle.ref() if oracle.ref_available() else None
+    cpu_model, physical, counts = thread_counts()
+    threads = counts[-1]
+    shapes = [(2048, 2048), (256, 2048), (5632, 2048), (2048, 5632), (4096, 4096)]
+    for m in lines:
+        base = None
+        if ref is not None and m["kernel"] == "matvec_q":
+            rows, cols = m["shape"]
+            i = shapes.index((rows, cols))
+            w = nut.synth_normal(2, 100 + i, rows * cols, 0.02)
+            x = nut.synth_normal(2, 200 + i, cols, 1.0)
+            qt = 1 if m["type"] == "int4" else 0
+            sec = oracle.C.c_double()
+            oracle.check(ref.ref_matvec_q_time(oracle.ptr(w), rows, cols, qt, oracle.ptr(x),
+                                               threads, 50, oracle.C.byref(sec)))
+            base = {"value": round(m["bytes_per_launch"] / sec.value / 1e9, 2),
+                    "unit": "GB/s", "cores": threads, "kind": "reference",
+                    "cpu_model": cpu_model,
+                    "sample": f"median of 50 matvec_quantized_threaded calls, "
+                              f"{threads} threads"}
+        elif ref is not None and m["kernel"] == "matmul_f32":
+            n = m["shape"][0]
+            a = nut.synth_normal(7, 1, n * n, 1.0)
+            b = nut.synth_normal(7, 2, n * n, 1.0)
+            sec = oracle.C.c_double()
+            oracle.check(ref.ref_matmul_time(oracle.ptr(a), oracle.ptr(b), n, n, n,
+                                             threads, 5, oracle.C.byref(sec)))
+            base = {"value": round(m["flop_per_call"] / sec.value / 1e12, 4),
+                    "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+                    "cpu_model": cpu_model,
+                    "sample": f"median of 5 matmul_threaded calls, {threads} threads"}
+        m["cpu_baseline"] = base
+        print(json.dumps(m), flush=True)
+    del np
 
 
 def main():
@@ -156,11 +321,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
     ap.add_argument("--workload", default="tinyllama_int4",
-                    choices=["tinyllama_int4", "tinyllama_int8_2k",
-                             "llama7b_int4"],
-                    help="tinyllama_int4 (default): the headline line below; "
-                         "the others print one line of prefill and decode "
-                         "tok/s for the long-prompt configurations")
+                    choices=["tinyllama_int4", "tinyllama_int8_2k", "llama7b_int4",
+                             "kernels"],
+                    help="tinyllama_int4 (default): the headline line; the others "
+                         "print the long-prompt lines or the standalone kernels")
     ap.add_argument("--prefill-only", action="store_true",
                     help="long-prompt workloads: time the batched prefill "
                          "alone (host clock), for kernel traces")
@@ -184,6 +348,9 @@ def main():
     if nut.device_count() < 1:
         print("no gfx950 device", file=sys.stderr)
         sys.exit(1)
+    if args.workload == "kernels":
+        kernels(args)
+        return
     if args.workload != "tinyllama_int4":
         long_prompt(args, nut, workloads)
         return
@@ -228,7 +395,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(value / PUBLISHED_DECODE_TOK_S, 3),
-        "dtype": "fp32",
+        "dtype": "int4",
         "data": "synthetic (seeded N(0,0.02) weights, uniform prompt ids)",
         "config": {
             "workload": "TinyLlama-1.1B-shape INT4 block-32 greedy decode",

@@ -91,6 +91,8 @@ _REF = {
     "ref_fmodel_add_layer": (C.c_int, [_P] * 10),
     "ref_fmodel_free": (None, [_P]),
     "ref_fmodel_run": (C.c_int, [_P, _P, _SZ, _P, _SZ, _SZ, _P, _P, _P, _P]),
+    "ref_matvec_q_time": (C.c_int, [_P, _SZ, _SZ, C.c_int, _P, _SZ, _SZ, _P]),
+    "ref_decode_time": (C.c_int, [_P, _SZ, _P, _SZ, _SZ, _P]),
     "ref_generate_sampled": (C.c_int, [_P, _P, _SZ, _SZ, _SZ, C.c_float, C.c_float,
                                        C.c_uint, _P, _P]),
 }
@@ -344,6 +346,14 @@ class RefModel:
                                          ptr(out), C.byref(count)),
               "ref_generate_sampled")
         return out[:count.value].tolist()
+
+    def decode_time(self, start_length, tokens, threads):
+        """Seconds of len(tokens) decode-loop steps from start_length."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        sec = C.c_double()
+        check(ref().ref_decode_time(self.handle, start_length, ptr(t), t.size,
+                                    threads, C.byref(sec)), "ref_decode_time")
+        return sec.value
 
     def storage_bytes(self):
         return ref().ref_model_storage_bytes(self.handle)

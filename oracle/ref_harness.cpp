@@ -147,6 +147,27 @@ int ref_matmul_time(const float *a, const float *b, size_t m, size_t k,
     GUARD_END
 }
 
+/* Time matvec_quantized_threaded on a matrix quantised once by the
+ * reference: the median seconds of `repeats` calls. */
+int ref_matvec_q_time(const float *source, size_t rows, size_t cols, int type,
+                      const float *x, size_t threads, size_t repeats, double *median)
+{
+    GUARD_BEGIN
+    QuantizedMatrix q = QuantizedMatrix::quantize(source, rows, cols, qtype(type), 32);
+    std::vector<float> y(rows);
+    std::vector<double> times;
+    matvec_quantized_threaded(q, x, y.data(), threads);
+    for (size_t i = 0; i < repeats; i++) {
+        const auto t0 = std::chrono::steady_clock::now();
+        matvec_quantized_threaded(q, x, y.data(), threads);
+        times.push_back(std::chrono::duration<double>(std::chrono::steady_clock::now() - t0)
+                            .count());
+    }
+    std::sort(times.begin(), times.end());
+    *median = times[times.size() / 2];
+    GUARD_END
+}
+
 int ref_rmsnorm(const float *x, const float *w, float *out, size_t n,
                 float eps)
 {
@@ -304,6 +325,33 @@ int ref_generate(void *handle, const int *prompt, size_t n, size_t max_tokens,
     *count = ids.size();
     *prefill_seconds = stats.prefill_seconds;
     *decode_seconds = stats.decode_seconds;
+    GUARD_END
+}
+
+/* The decode loop of generate_tokens_cached (src/generate.cpp:194-207:
+ * final rmsnorm, classifier, argmax, decode_quantized_token) for n steps
+ * from a cache whose length is set to start_length (a decode step costs the
+ * same whatever the cached rows hold), feeding tokens[i]; seconds gets the
+ * wall time of the n steps. */
+int ref_decode_time(void *handle, size_t start_length, const int *tokens, size_t n,
+                    size_t threads, double *seconds)
+{
+    GUARD_BEGIN
+    const QuantizedModelWeights &m = *static_cast<RefModel *>(handle)->weights;
+    const ModelConfig &c = m.config;
+    KVCache cache(c);
+    cache.set_length(start_length);
+    std::vector<float> last(c.dim, 0.01f), normalized(c.dim), logits(c.vocab_size);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (size_t i = 0; i < n; i++) {
+        rmsnorm(last.data(), m.final_norm.data(), normalized.data(), c.dim, 1e-5f);
+        matvec_threaded(m.output_weights(), normalized.data(), logits.data(), threads);
+        volatile size_t best =
+            size_t(std::max_element(logits.begin(), logits.end()) - logits.begin());
+        (void)best;
+        last = decode_quantized_token(m, tokens[i], cache, threads);
+    }
+    *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     GUARD_END
 }
 
