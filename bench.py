@@ -52,9 +52,9 @@ PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 
 # HBM bytes one generate launch (16 iterations) moves, from rocprofv3
 # counter runs of this bench (profiles/token_kernel_tinyllama_int4_decode.md):
-# FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB, the scales read off a 1 GiB
+# FETCH_SIZE x 1.99993 + WRITE_SIZE x 1.0 KiB, the scales read off a 1 GiB
 # device-to-device copy in the same runs.
-MEASURED_TRAFFIC_BYTES = 13_535_426_731
+MEASURED_TRAFFIC_BYTES = 13_535_409_278
 CPU_SAMPLE_SECONDS = 8.0
 MAX_THREADS = 16  # the GPU box's CPU share
 
