@@ -543,6 +543,7 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.x_part = a.x_act + s.ffn_dim;
     a.x_apart = a.x_part + 2 * kTokenGrid;
     a.x_ctx = a.x_apart + size_t(kTokenGrid) * (s.heads / s.kv_heads) * (s.head_dim + 2);
+    a.x_scores = wide_kernel_score_entries(s) > 0 ? a.x_ctx + s.dim : nullptr;
     // beyond the fused attention pass, attention is split over the grid
     a.long_attention =
         start + n_iter > size_t(token_kernel_max_positions(m.type, s)) ? 1 : 0;

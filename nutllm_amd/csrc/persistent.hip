@@ -23,18 +23,11 @@
 // waits observe, and every workgroup runs to the end.
 #include "persistent.hpp"
 #include "runtime.hpp"
+#include "token_device.hpp"
 
 namespace nut {
 
 namespace {
-
-constexpr int kGrid = kTokenGrid;
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kSpinLimit = 200000;
-
-constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
-constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int QT_, int DIM_, int FFN_, int HEADS_, int KVH_, int HD_, int NP_>
 struct Geo {
@@ -89,546 +82,6 @@ struct Geo {
                   "attention: 16 lanes per head row, a wave's heads share a kv head");
     static_assert((DIM + 2 * KVD) % 2 == 0 && KVD % 2 == 0, "row pairs");
 };
-
-// ------------------------------------------------------------ exchange --
-
-__device__ __forceinline__ uint64_t load_coherent(const uint64_t *p)
-{
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_coherent(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void put(uint64_t *p, float v, unsigned tag)
-{
-    __hip_atomic_store(p, (uint64_t(tag) << 32) | __float_as_uint(v),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ bool failed(const int *error)
-{
-    return __hip_atomic_load(error, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT) != 0;
-}
-
-// The error flag as seen by thread 0, made uniform over the workgroup so
-// every thread takes the same branch.
-__device__ __forceinline__ bool wg_failed(const int *error, int *slot)
-{
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *slot = failed(error) ? 1 : 0;
-    __syncthreads();
-    return *slot != 0;
-}
-
-// Re-poll *p until its tag matches (bounded; gives up once any wait failed).
-__device__ __noinline__ uint64_t wait_tag(const uint64_t *p, unsigned tag,
-                                          int *error)
-{
-    uint64_t v = load_coherent(p);
-    int spins = 0;
-    while (unsigned(v >> 32) != tag) {
-        __builtin_amdgcn_s_sleep(2);
-        v = load_coherent(p);
-        if ((++spins & 63) == 0 && failed(error))
-            break;
-        if (spins > kSpinLimit) {
-            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-    }
-    return v;
-}
-
-__device__ __forceinline__ int wave_index()
-{
-    return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-}
-
-// --------------------------------------------------------------- LDS DMA --
-
-// Copy `bytes` (a multiple of 16) from global memory to LDS without
-// registers: 1 KB per wave instruction, lane i moving bytes [16i, 16i+16) of
-// its kilobyte; instructions are spread over the workgroup's waves.
-// Completion: s_waitcnt vmcnt(0) in every wave, then a workgroup barrier.
-// The loads carry the non-temporal cache policy (nt, bit 1 of the
-// instruction's cache-policy field): each weight byte is read once per token,
-// and streaming it leaves the memory-side cache to the fp32 classifier, whose
-// rows then partly hit there on the next token (classifier pass 50 -> 44 us
-// for the TinyLlama shape).
-constexpr int kStreamPolicy = 2;
-
-__device__ __forceinline__ void dma(void *lds_dst, const void *src, int bytes)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    const int n = (bytes + 1023) >> 10;
-    for (int i = wave_index(); i < n; i += kWaves) {
-        const int off = (i << 10) + (lane << 4);
-        if (off < bytes)
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(
-                    static_cast<const char *>(src) + off),
-                (__attribute__((address_space(3))) void *)(
-                    static_cast<char *>(lds_dst) + (i << 10)),
-                16, 0, kStreamPolicy);
-    }
-}
-
-__device__ __forceinline__ void dma_wait()
-{
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-}
-
-// Rows [0, n) of 64-float rows at src into LDS rows of 68 floats (16 data
-// granules + 1 spare): LDS granule j holds row j / 17, granule j % 17.
-// POLICY is the loads' cache policy: 0 where every workgroup stages the
-// same rows (they stay in L2), kStreamPolicy where each row is staged by one
-// workgroup once per token.
-template <int POLICY = 0>
-__device__ __forceinline__ void dma_padded_rows(float *lds_dst,
-                                                const float *src, int n)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    const int instrs = (n * 17 + kWave - 1) / kWave;
-    for (int i = wave_index(); i < instrs; i += kWaves) {
-        const int j = i * kWave + lane;
-        const int row = j / 17, g = j - row * 17;
-        if (row < n && g < 16)
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(
-                    src + row * 64 + g * 4),
-                (__attribute__((address_space(3))) void *)(
-                    reinterpret_cast<char *>(lds_dst) + i * 1024),
-                16, 0, POLICY);
-    }
-}
-
-// --------------------------------------------------------- x staging --
-
-// Element i of x lives at swz(i): quads of each 32-element block are
-// rotated by the block index, so lane b reading quad q of block b hits a
-// different 16-byte bank group than lanes b+1..b+7.
-__device__ __forceinline__ int swz(int i)
-{
-    const int b = i >> 5, q = (i >> 2) & 7;
-    return (b << 5) | (((q + b) & 7) << 2) | (i & 3);
-}
-
-// Workgroup sum of per-thread values; every thread gets the total.
-__device__ __forceinline__ float wg_sum(float v, float *red)
-{
-    v = wave_total(v);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    __syncthreads();
-    if (lane == 0)
-        red[wave] = v;
-    __syncthreads();
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++)
-        total += red[w];
-    return total;
-}
-
-// Block sums of x (swizzled), for the offset-binary float dots.
-__device__ void block_sums(const float *xs, float *xsum, int n)
-{
-    for (int b = threadIdx.x; b < n / 32; b += kThreads) {
-        const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-            s += (base[q].x + base[q].y) + (base[q].z + base[q].w);
-        xsum[b] = s;
-    }
-    __syncthreads();
-}
-
-// x of a dim-sized phase as integer digits for the dot instructions. Per
-// 32-element block b with m = max |x_k|: X_k = rint(x_k * kLimbRange / m),
-// so x_k = xsc[b] * X_k to 2^-23.7 m, and X_k is written as signed digits,
-// six of 4 bits (INT4 rows, v_dot8_i32_i4) or three of 8 bits (INT8 rows,
-// v_dot4_i32_i8): X_k = sum_d digit_d 16^d (or 256^d). The digits come from
-// the offset form: for INT4, X + 0x888888 has hex digits e_d in 0..15 and
-// digit_d = e_d - 8, which as a 4-bit two's-complement field is e_d ^ 8, so
-// (X + 0x888888) ^ 0x888888 holds the six digits as nibbles (|X| <= 7e6
-// keeps X + 0x888888 in 0..2^24); INT8 likewise with 0x808080. Block b's
-// kLimbWords words at xl + kLimbStride * b: INT4 word 4 d + j holds digit d
-// of elements 8 j .. 8 j + 7 (nibble t = element 8 j + t, the weights'
-// nibble order); INT8 word 8 d + j digit d of elements 4 j .. 4 j + 3. A
-// NaN or infinity in a block makes xsc[b] NaN.
-constexpr float kLimbRange = 7.0e6f;
-constexpr int kLimbWords = 24;
-constexpr int kLimbStride = 28; // words; lanes b .. b + 15 hit distinct banks
-
-// Digits of quartet q (elements 4 q .. 4 q + 3) of block b, from the lane
-// holding it; the block's eight quartets sit in lanes 8 k .. 8 k + 7 of one
-// wave (DPP reduces the block maximum), all lanes of the wave take part.
-template <int QT>
-__device__ __forceinline__ void quartet_digits(float4 v, int b, int q, uint32_t *xl,
-                                               float *xsc)
-{
-    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    float poison = ((v.x + v.y) + (v.z + v.w)) * 0.0f; // NaN for NaN or inf
-    mx = fmaxf(mx, dpp<kDppQuadSwap1>(mx, 0.0f));
-    mx = fmaxf(mx, dpp<kDppQuadSwap2>(mx, 0.0f));
-    mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx, 0.0f));
-    poison += dpp<kDppQuadSwap1>(poison, 0.0f);
-    poison += dpp<kDppQuadSwap2>(poison, 0.0f);
-    poison += dpp<kDppRowHalfMirror>(poison, 0.0f);
-    // r within an ulp of kLimbRange / mx: x_k = xsc X_k holds to 2^-23
-    const float r = mx > 0.0f ? kLimbRange * __builtin_amdgcn_rcpf(mx) : 0.0f;
-    if (q == 0)
-        xsc[b] = mx * (1.0f / kLimbRange) + poison;
-    // X + offset in one FMA (exact below 2^24 up to its rounding) and one
-    // conversion: v_cvt_rpi_i32_f32 is floor(v + 0.5)
-    constexpr uint32_t kOff = QT == 1 ? 0x888888u : 0x808080u;
-    const float xv[4] = {v.x, v.y, v.z, v.w};
-    uint32_t y[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int c;
-        asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(c) : "v"(fmaf(xv[k], r, float(kOff))));
-        y[k] = uint32_t(c) ^ kOff;
-    }
-    // P[i] = byte i of y[0..3], one per byte
-    const uint32_t a01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
-    const uint32_t a23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
-    const uint32_t c01 = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0602u);
-    const uint32_t c23 = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0602u);
-    const uint32_t P[3] = {__builtin_amdgcn_perm(a23, a01, 0x05040100u),
-                           __builtin_amdgcn_perm(a23, a01, 0x07060302u),
-                           __builtin_amdgcn_perm(c23, c01, 0x05040100u)};
-    uint32_t *blk = xl + kLimbStride * b;
-    if (QT == 1) {
-        // digit 2 i is the low nibble of byte i, 2 i + 1 the high one; the
-        // quartet is nibbles 4 (q & 1) .. 4 (q & 1) + 3 of word (d, q >> 1)
-        uint16_t *half = reinterpret_cast<uint16_t *>(blk + (q >> 1)) + (q & 1);
-#pragma unroll
-        for (int i = 0; i < 3; i++) {
-#pragma unroll
-            for (int hi = 0; hi < 2; hi++) {
-                const uint32_t n = (hi ? P[i] >> 4 : P[i]) & 0x0f0f0f0fu;
-                const uint32_t m = n | (n >> 4); // nibble pairs in bytes 0, 2
-                half[2 * 4 * (2 * i + hi)] =
-                    uint16_t(__builtin_amdgcn_perm(0u, m, 0x0c0c0200u));
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 3; i++)
-            blk[8 * i + q] = P[i];
-    }
-}
-
-// This thread's elements i = threadIdx.x + kThreads * u of an N-vector in
-// global memory, in registers; loads issued together (no dependent waits).
-template <int N> struct Slice {
-    static constexpr int PER = cdiv(N, kThreads);
-    float v[PER];
-    __device__ __forceinline__ void load(const float *src)
-    {
-#pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int i = threadIdx.x + u * kThreads;
-            v[u] = i < N ? src[i] : 0.0f;
-        }
-    }
-    // dst[i] = v, returns this thread's sum of squares.
-    __device__ __forceinline__ float store(float *dst) const
-    {
-        float sq = 0.0f;
-#pragma unroll
-        for (int u = 0; u < PER; u++) {
-            const int i = threadIdx.x + u * kThreads;
-            if (i < N) {
-                dst[i] = v[u];
-                sq = fmaf(v[u], v[u], sq);
-            }
-        }
-        return sq;
-    }
-};
-
-// Digits (quartet_digits) of x = src * scale * w for a dim of 4 kThreads:
-// thread t takes elements 4 t .. 4 t + 3, w holding its four weights.
-// Ends with a barrier.
-template <int QT, int N>
-__device__ void stage_x(const float *src, float4 w, float scale, uint32_t *xl,
-                        float *xsc)
-{
-    static_assert(N == 4 * kThreads, "one quartet per thread");
-    const float4 h = reinterpret_cast<const float4 *>(src)[threadIdx.x];
-    const float4 x = make_float4(h.x * scale * w.x, h.y * scale * w.y, h.z * scale * w.z,
-                                 h.w * scale * w.w);
-    quartet_digits<QT>(x, threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
-    __syncthreads();
-}
-
-__device__ __forceinline__ float rms_scale(float squares, int n)
-{
-    return 1.0f / sqrtf(squares / float(n) + 1e-5f);
-}
-
-// dst[map(i)] = value of src[i] once tagged, i < N; returns this thread's
-// sum of squares. A thread's loads are issued together, and every round
-// re-issues all of its still-stale loads together, so a late producer costs
-// one coherent round trip per round rather than one per element. Bounded:
-// gives up once any wait failed. Waits for this wave's outstanding DMA, then
-// a barrier.
-template <int N, bool SWIZZLE>
-__device__ float take(const uint64_t *src, float *dst, unsigned tag,
-                      int *error)
-{
-    constexpr int PER = cdiv(N, kThreads);
-    uint64_t v[PER];
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        const int i = threadIdx.x + u * kThreads;
-        v[u] = i < N ? load_coherent(src + i) : uint64_t(tag) << 32;
-    }
-    for (int spins = 0;; spins++) {
-        bool stale = false;
-#pragma unroll
-        for (int u = 0; u < PER; u++)
-            stale |= unsigned(v[u] >> 32) != tag;
-        if (!stale)
-            break;
-        if ((spins & 63) == 63 && failed(error))
-            break;
-        if (spins > kSpinLimit) {
-            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int u = 0; u < PER; u++)
-            if (unsigned(v[u] >> 32) != tag)
-                v[u] = load_coherent(src + threadIdx.x + u * kThreads);
-    }
-    float squares = 0.0f;
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        const int i = threadIdx.x + u * kThreads;
-        if (i < N) {
-            const float f = __uint_as_float(unsigned(v[u]));
-            dst[SWIZZLE ? swz(i) : i] = f;
-            squares = fmaf(f, f, squares);
-        }
-    }
-    dma_wait();
-    return squares;
-}
-
-// ------------------------------------------------------ quantised rows --
-
-// sum_k u_k x_k over one INT4 block (u = q + 8, offset binary). The high
-// nibbles are converted in place (16 u), and their accumulator is scaled by
-// 1/16 once: power-of-two scaling commutes with rounding, so the result is
-// the same as accumulating u x.
-__device__ __forceinline__ float dot_block_int4(const uint4 &w,
-                                                const float4 (&x)[8])
-{
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t lo = opaque((words[j] ^ 0x88888888u) & 0x0f0f0f0fu);
-        const uint32_t hi = opaque((words[j] ^ 0x88888888u) & 0xf0f0f0f0u);
-        const float4 xa = x[2 * j], xb = x[2 * j + 1];
-        a0 = fmaf(ubyte0(lo), xa.x, a0);
-        a1 = fmaf(ubyte0(hi), xa.y, a1);
-        a0 = fmaf(ubyte1(lo), xa.z, a0);
-        a1 = fmaf(ubyte1(hi), xa.w, a1);
-        a0 = fmaf(ubyte2(lo), xb.x, a0);
-        a1 = fmaf(ubyte2(hi), xb.y, a1);
-        a0 = fmaf(ubyte3(lo), xb.z, a0);
-        a1 = fmaf(ubyte3(hi), xb.w, a1);
-    }
-    return fmaf(a1, 0.0625f, a0);
-}
-
-__device__ __forceinline__ float dot_block_int8(const uint4 &w0,
-                                                const uint4 &w1,
-                                                const float4 (&x)[8])
-{
-    const uint32_t words[8] = {w0.x ^ 0x80808080u, w0.y ^ 0x80808080u,
-                               w0.z ^ 0x80808080u, w0.w ^ 0x80808080u,
-                               w1.x ^ 0x80808080u, w1.y ^ 0x80808080u,
-                               w1.z ^ 0x80808080u, w1.w ^ 0x80808080u};
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        a0 = fmaf(ubyte0(words[j]), x[j].x, a0);
-        a1 = fmaf(ubyte1(words[j]), x[j].y, a1);
-        a0 = fmaf(ubyte2(words[j]), x[j].z, a0);
-        a1 = fmaf(ubyte3(words[j]), x[j].w, a1);
-    }
-    return a0 + a1;
-}
-
-// Wave dot product of a staged row with x (swizzled floats in LDS, block
-// sums xsum): per block, offset-binary codes against x minus the bias times
-// the block sum, times the block's fp16 scale. Used where x is ffn-sized:
-// staging its digits would cost more than the float dot.
-template <int QT, int CPL>
-__device__ __forceinline__ float row_dot_floats(const uint8_t *row,
-                                                const uint16_t *scales,
-                                                const float *xs,
-                                                const float *xsum, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks) {
-            float4 xq[8];
-            const float4 *base = reinterpret_cast<const float4 *>(xs + (b << 5));
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                xq[q] = base[(q + b) & 7];
-            float d;
-            if (QT == 1) {
-                d = dot_block_int4(reinterpret_cast<const uint4 *>(row)[b], xq) -
-                    8.0f * xsum[b];
-            } else {
-                const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
-                d = dot_block_int8(p[0], p[1], xq) - 128.0f * xsum[b];
-            }
-            acc += half_bits_to_float(scales[b]) * d;
-        }
-    }
-    return wave_total(acc);
-}
-
-// One block of a staged row (its two's-complement codes as stored) dotted
-// with the block's digits, exactly in integers per digit: every digit sum
-// is at most 32 * 7 * 8 (INT4) or 32 * 127 * 128 (INT8) in magnitude, and
-// the weighted sums below stay inside int32; the one or two conversions to
-// float round once each.
-template <int QT>
-__device__ __forceinline__ float dot_block_digits(const uint8_t *row, int b,
-                                                  const uint4 (&d)[6])
-{
-    if (QT == 1) {
-        const uint4 w = reinterpret_cast<const uint4 *>(row)[b];
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-        int acc[6];
-#pragma unroll
-        for (int i = 0; i < 6; i++) {
-            const uint32_t ds[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
-            acc[i] = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i] = __builtin_amdgcn_sdot8(int(ws[j]), int(ds[j]), acc[i], false);
-        }
-        const int lo = acc[0] + acc[1] * 16 + acc[2] * 256;
-        const int hi = acc[3] + acc[4] * 16 + acc[5] * 256;
-        return fmaf(float(hi), 4096.0f, float(lo));
-    } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(row) + 2 * b;
-        const uint4 w0 = p[0], w1 = p[1];
-        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        int acc[3];
-#pragma unroll
-        for (int i = 0; i < 3; i++) {
-            const uint32_t ds[8] = {d[2 * i].x, d[2 * i].y, d[2 * i].z, d[2 * i].w,
-                                    d[2 * i + 1].x, d[2 * i + 1].y, d[2 * i + 1].z,
-                                    d[2 * i + 1].w};
-            acc[i] = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                acc[i] = __builtin_amdgcn_sdot4(int(ws[j]), int(ds[j]), acc[i], false);
-        }
-        const int lo = acc[0] + acc[1] * 256;
-        return fmaf(float(acc[2]), 65536.0f, float(lo));
-    }
-}
-
-__device__ __forceinline__ void load_digits(const uint32_t *xl, int b, uint4 (&d)[6])
-{
-    const uint4 *p = reinterpret_cast<const uint4 *>(xl + kLimbStride * b);
-#pragma unroll
-    for (int i = 0; i < 6; i++)
-        d[i] = p[i];
-}
-
-// x of one phase held in registers as digits, lane's blocks b = lane + 64 j.
-template <int CPL> struct XDigits {
-    uint4 d[CPL][6];
-    float sc[CPL];
-};
-
-template <int CPL>
-__device__ __forceinline__ void load_x(XDigits<CPL> &x, const uint32_t *xl,
-                                       const float *xsc, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks) {
-            load_digits(xl, b, x.d[j]);
-            x.sc[j] = xsc[b];
-        }
-    }
-}
-
-// Wave dot product of a staged row with x in registers; all lanes get it.
-// Block b contributes (its fp16 scale) * xsc[b] * (integer block dot).
-template <int QT, int CPL>
-__device__ __forceinline__ float row_dot(const uint8_t *row,
-                                         const uint16_t *scales,
-                                         const XDigits<CPL> &x, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks)
-            acc = fmaf(half_bits_to_float(scales[b]) * x.sc[j],
-                       dot_block_digits<QT>(row, b, x.d[j]), acc);
-    }
-    return wave_total(acc);
-}
-
-// As row_dot, reading the digits from LDS (rows swept once per wave).
-template <int QT, int CPL>
-__device__ __forceinline__ float row_dot_lds(const uint8_t *row,
-                                             const uint16_t *scales,
-                                             const uint32_t *xl,
-                                             const float *xsc, int blocks)
-{
-    const int lane = threadIdx.x & (kWave - 1);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int b = lane + kWave * j;
-        if (b < blocks) {
-            uint4 d[6];
-            load_digits(xl, b, d);
-            acc = fmaf(half_bits_to_float(scales[b]) * xsc[b],
-                       dot_block_digits<QT>(row, b, d), acc);
-        }
-    }
-    return wave_total(acc);
-}
-
-// Units [begin, end) of `units` owned by this workgroup.
-__device__ __forceinline__ void wg_share(int units, int &begin, int &end)
-{
-    begin = int((long long)units * blockIdx.x / kGrid);
-    end = int((long long)units * (blockIdx.x + 1) / kGrid);
-}
 
 // ------------------------------------------------- split attention --
 
@@ -904,110 +357,14 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     xs[i] = h_raw[i] * scale * nw.v[u];
             }
             __syncthreads();
-            constexpr int C4 = G::DIM / 4 / kWave; // float4 per lane per row
-            const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-            int rb, re;
-            {
-                int wb, we;
-                wg_share(a.vocab, wb, we);
-                rb = wb + (we - wb) * wave / kWaves;
-                re = wb + (we - wb) * (wave + 1) / kWaves;
-            }
-            float best_v = -INFINITY;
-            int best_i = 0x7fffffff;
-            for (int row = rb; row < re; row += 2) {
-                const bool two = row + 1 < re;
-                const float4 *w0 = reinterpret_cast<const float4 *>(wcls + size_t(row) * G::DIM);
-                const float4 *w1 = reinterpret_cast<const float4 *>(wcls + size_t(two ? row + 1 : row) * G::DIM);
-                float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-                for (int j0 = 0; j0 < C4; j0 += 4) {
-                    float4 v0[4], v1[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        v0[j] = w0[lane + kWave * (j0 + j)];
-                        v1[j] = w1[lane + kWave * (j0 + j)];
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const float4 x = x4[lane + kWave * (j0 + j)];
-                        s0 = fmaf(v0[j].x, x.x, s0);
-                        s0 = fmaf(v0[j].y, x.y, s0);
-                        s0 = fmaf(v0[j].z, x.z, s0);
-                        s0 = fmaf(v0[j].w, x.w, s0);
-                        s1 = fmaf(v1[j].x, x.x, s1);
-                        s1 = fmaf(v1[j].y, x.y, s1);
-                        s1 = fmaf(v1[j].z, x.z, s1);
-                        s1 = fmaf(v1[j].w, x.w, s1);
-                    }
-                }
-                s0 = wave_total(s0);
-                s1 = wave_total(s1);
-                if (s0 > best_v) {
-                    best_v = s0;
-                    best_i = row;
-                }
-                if (two && s1 > best_v) {
-                    best_v = s1;
-                    best_i = row + 1;
-                }
-            }
+            float best_v;
+            int best_i;
+            classifier_best<G::DIM>(wcls, xs, a.vocab, best_v, best_i);
             __syncthreads();
             // Layer 0's QKV rows stream into LDS during the argmax exchange.
             stage_qkv(0);
-            if (lane == 0) {
-                red[wave] = best_v;
-                misc[wave] = best_i;
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                float bv = red[0];
-                int bi = misc[0];
-                for (int w = 1; w < kWaves; w++)
-                    if (red[w] > bv || (red[w] == bv && misc[w] < bi)) {
-                        bv = red[w];
-                        bi = misc[w];
-                    }
-                // the block's best (value, index) as two tagged words
-                put(a.x_part + blockIdx.x, bv, tag);
-                put(a.x_part + kGrid + blockIdx.x, __int_as_float(bi), tag);
-            }
-            // every workgroup reduces all partials to the same token
-            float pv = -INFINITY;
-            int pi = 0x7fffffff;
-            if (threadIdx.x < kGrid) {
-                uint64_t v = load_coherent(a.x_part + threadIdx.x);
-                uint64_t i = load_coherent(a.x_part + kGrid + threadIdx.x);
-                if (unsigned(v >> 32) != tag)
-                    v = wait_tag(a.x_part + threadIdx.x, tag, error);
-                if (unsigned(i >> 32) != tag)
-                    i = wait_tag(a.x_part + kGrid + threadIdx.x, tag, error);
-                pv = __uint_as_float(unsigned(v));
-                pi = int(unsigned(i));
-            }
+            const int bi = argmax_exchange(a.x_part, best_v, best_i, red, misc, tag, error);
             tag++;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(pv, off);
-                const int oi = __shfl_xor(pi, off);
-                if (ov > pv || (ov == pv && oi < pi)) {
-                    pv = ov;
-                    pi = oi;
-                }
-            }
-            __syncthreads();
-            if (lane == 0) {
-                red[wave] = pv;
-                misc[wave] = pi;
-            }
-            __syncthreads();
-            float bv = red[0];
-            int bi = misc[0];
-            for (int w = 1; w < kWaves; w++)
-                if (red[w] > bv || (red[w] == bv && misc[w] < bi)) {
-                    bv = red[w];
-                    bi = misc[w];
-                }
             token = (bi >= 0 && bi < a.vocab) ? bi : 0;
             if (wg_failed(error, misc + 8))
                 break;
@@ -1377,7 +734,8 @@ void launch(const TokenArgs &args, hipStream_t stream)
 
 bool token_kernel_supported(int type, const DecodeShape &s)
 {
-    if (!(shape_is<TinyLlamaInt4>(s, type) || shape_is<TinyLlamaInt8>(s, type)))
+    if (!(shape_is<TinyLlamaInt4>(s, type) || shape_is<TinyLlamaInt8>(s, type) ||
+          wide_kernel_positions(type, s) > 0))
         return false;
     return device_cus() >= kGrid;
 }
@@ -1388,7 +746,7 @@ int token_kernel_max_positions(int type, const DecodeShape &s)
         return TinyLlamaInt4::NP;
     if (shape_is<TinyLlamaInt8>(s, type))
         return TinyLlamaInt8::NP;
-    return 0;
+    return wide_kernel_positions(type, s);
 }
 
 int token_kernel_long_positions(int type, const DecodeShape &s)
@@ -1397,16 +755,17 @@ int token_kernel_long_positions(int type, const DecodeShape &s)
         return TinyLlamaInt4::SPLITS * TinyLlamaInt4::PMAX;
     if (shape_is<TinyLlamaInt8>(s, type))
         return TinyLlamaInt8::SPLITS * TinyLlamaInt8::PMAX;
-    return 0;
+    return wide_kernel_positions(type, s);
 }
 
 size_t token_exchange_entries(const DecodeShape &s)
 {
     const size_t kvd = size_t(s.kv_heads) * s.head_dim;
     const size_t group = s.heads / (s.kv_heads == 0 ? s.heads : s.kv_heads);
-    // q/k/v, h, act, classifier partials; split attention partials, context
+    // q/k/v, h, act, classifier partials; split attention partials, context;
+    // the wide kernel's partial scores
     return (s.dim + 2 * kvd) + s.dim + s.ffn_dim + 2 * kGrid +
-           size_t(kGrid) * group * (s.head_dim + 2) + s.dim;
+           size_t(kGrid) * group * (s.head_dim + 2) + s.dim + wide_kernel_score_entries(s);
 }
 
 void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,
@@ -1416,6 +775,8 @@ void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,
         launch<TinyLlamaInt4>(a, stream);
     else if (shape_is<TinyLlamaInt8>(s, type))
         launch<TinyLlamaInt8>(a, stream);
+    else if (wide_kernel_positions(type, s) > 0)
+        launch_wide_kernel(type, s, a, stream);
     else
         fail(NUT_EINVAL, "token kernel: unsupported shape");
 }

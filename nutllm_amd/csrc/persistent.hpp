@@ -28,6 +28,9 @@ struct TokenArgs {
     // query heads of its KV head, x_ctx the merged context.
     uint64_t *x_apart, *x_ctx;
     int long_attention;
+    // Wide shapes (wide.hip): each workgroup's partial attention scores,
+    // [head][workgroup of the head][position].
+    uint64_t *x_scores;
     const float *hidden_in;   // hidden state before iteration 0 (classify)
     float *hidden_out;        // hidden state after the last decode step
     const int *tokens_in;     // per-iteration tokens (prefill)
@@ -95,5 +98,13 @@ bool token_kernel_supported(int type, const DecodeShape &s);
 size_t token_exchange_entries(const DecodeShape &s);
 void launch_token_kernel(int type, const DecodeShape &s, const TokenArgs &a,
                          hipStream_t stream);
+
+// The kernel for wide multi-head shapes (wide.hip): its longest context (0
+// when the shape and type have no instantiation), the uint64 entries of its
+// score buffer (TokenArgs::x_scores; 0 for other shapes), and its launch.
+int wide_kernel_positions(int type, const DecodeShape &s);
+size_t wide_kernel_score_entries(const DecodeShape &s);
+void launch_wide_kernel(int type, const DecodeShape &s, const TokenArgs &a,
+                        hipStream_t stream);
 
 } // namespace nut

@@ -19,6 +19,15 @@ Mark k of layer l is column 2 + 13 l + k of ``timeline()``: 0 A input
 ready, 1 A published, 2 DMA issued, 3 B input ready, 4 attention done,
 5 B published, 6 DMA issued, 7 C input ready, 8 C published, 9 DMA
 issued, 10 D input ready, 11 D published, 12 next DMA issued.
+
+Wide multi-head shapes run the kernel of wide.hip, whose marks are: 0 A
+input ready, 1 q/k/v published, 2 partial scores published (V and Wo
+rows issued), 3 context published, 4 Wo input ready, 5 Wo published,
+6 C input ready (gate/up rows issued before the wait), 7 C published,
+8 D input ready (W2 rows issued before the wait), 9 D published, 10 and
+12 layer end (the next layer's q/k/v rows are issued before its wait);
+the printout is then the median of each segment between consecutive
+marks.
 """
 import sys
 
@@ -60,6 +69,35 @@ def summarise(t, layers):
     return out
 
 
+WIDE_SEGMENTS = [("A issue + h exchange", -1, 0), ("A rows", 0, 1),
+                 ("V/Wo issue + partial scores", 1, 2),
+                 ("score exchange + softmax + context", 2, 3),
+                 ("context exchange", 3, 4), ("Wo rows", 4, 5),
+                 ("gate/up issue + h exchange", 5, 6), ("gate/up rows", 6, 7),
+                 ("W2 issue + act exchange", 7, 8), ("W2 rows", 8, 9),
+                 ("layer end", 9, 12)]
+
+
+def summarise_wide(t, layers):
+    """The wide kernel's segments: mark -1 is the previous layer's end."""
+    its = range(2, t.shape[1] - 1)
+    col = lambda l, k: 2 + MARKS * l + k
+    out = {}
+    for name, a, b in WIDE_SEGMENTS:
+        d = []
+        for it in its:
+            for l in range(1 if a < 0 else 0, layers):
+                start = t[:, it, col(l - 1, 12)] if a < 0 else t[:, it, col(l, a)]
+                d.append(t[:, it, col(l, b)] - start)
+        out[name] = float(np.median(np.concatenate(d)))
+    lay = [np.median(t[:, it, col(l + 1, 0)] - t[:, it, col(l, 0)])
+           for it in its for l in range(layers - 1)]
+    out["layer"] = float(np.median(lay))
+    out["classifier + argmax"] = float(np.median([np.median(t[:, it, 2] - t[:, it, 0])
+                                                  for it in its]))
+    return out
+
+
 def main(argv):
     name = argv[1] if len(argv) > 1 else "tinyllama_int4"
     model, prompt, gen = workloads.build_run(name)
@@ -76,7 +114,10 @@ def main(argv):
         # own exit handlers run
         dev.close()
     print(f"{name}: {n} tokens, {ms * 1e3 / n:.1f} us per token (HIP events)")
-    for key, v in summarise(t, model.config.layers).items():
+    c = model.config
+    wide = c.kv_heads in (0, c.heads) and c.head_dim == 128
+    summary = summarise_wide if wide else summarise
+    for key, v in summary(t, c.layers).items():
         print(f"  {key:24s} {v:6.2f} us")
 
 
