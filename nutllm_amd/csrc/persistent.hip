@@ -560,9 +560,33 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 }
                 total = row16_sum(total);
                 // context: lanes of head hh own quad r of its output row
+                // (even and odd positions in two accumulators, eight
+                // positions' loads in flight)
                 const float4 *v4 = reinterpret_cast<const float4 *>(vg) + r;
                 float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                for (int p = 0; p < n; p++) {
+                float4 acc1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                int p = 0;
+                for (; p + 8 <= n; p += 8) {
+                    float4 v[8];
+                    float w[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        v[j] = v4[(p + j) * (G::KROW / 4)];
+                        w[j] = sc[p + j];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; j += 2) {
+                        acc.x = fmaf(w[j], v[j].x, acc.x);
+                        acc.y = fmaf(w[j], v[j].y, acc.y);
+                        acc.z = fmaf(w[j], v[j].z, acc.z);
+                        acc.w = fmaf(w[j], v[j].w, acc.w);
+                        acc1.x = fmaf(w[j + 1], v[j + 1].x, acc1.x);
+                        acc1.y = fmaf(w[j + 1], v[j + 1].y, acc1.y);
+                        acc1.z = fmaf(w[j + 1], v[j + 1].z, acc1.z);
+                        acc1.w = fmaf(w[j + 1], v[j + 1].w, acc1.w);
+                    }
+                }
+                for (; p < n; p++) {
                     const float4 v = v4[p * (G::KROW / 4)];
                     const float w = sc[p];
                     acc.x = fmaf(w, v.x, acc.x);
@@ -570,6 +594,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     acc.z = fmaf(w, v.z, acc.z);
                     acc.w = fmaf(w, v.w, acc.w);
                 }
+                acc.x += acc1.x;
+                acc.y += acc1.y;
+                acc.z += acc1.z;
+                acc.w += acc1.w;
                 const float inv = 1.0f / total;
                 const int e0 = head * G::HD + 4 * r;
                 quartet_digits<G::QT>(make_float4(acc.x * inv, acc.y * inv, acc.z * inv,
