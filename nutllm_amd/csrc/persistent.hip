@@ -25,9 +25,20 @@
 #include "runtime.hpp"
 #include "token_device.hpp"
 
+
 namespace nut {
 
 namespace {
+
+// Wait before each exchange's first poll, in 10 ns ticks of s_memrealtime.
+// A workgroup that polls right after its own publish re-reads words most
+// producers have not written yet, and 256 workgroups doing so flood the
+// memory system with coherent reads that slow every producer's publish and
+// every consumer's later rounds. Measured per exchange (TinyLlama INT4, 16
+// tokens; 423 us per token with no delay, 388 with these): into phases A
+// (h after W2) and D (act) 450 ns, into B (q/k/v) and C (h after Wo), which
+// follow a larger weight DMA that already delays their polls, 150 ns.
+constexpr int kPollDelayA = 45, kPollDelayB = 15, kPollDelayC = 15, kPollDelayD = 45;
 
 template <int QT_, int DIM_, int FFN_, int HEADS_, int KVH_, int HD_, int NP_>
 struct Geo {
@@ -405,7 +416,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = e.store(h_raw);
                 dma_wait();
             } else {
-                sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
+                sq = take<G::DIM, false, false, kPollDelayA>(a.x_hidden, h_raw, tag - 1, error);
             }
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 2 + 13 * l);
@@ -477,7 +488,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
-            take<G::DIM + 2 * G::KVD, false>(a.x_qkv, qkv, tag - 1, error);
+            take<G::DIM + 2 * G::KVD, false, false, kPollDelayB>(a.x_qkv, qkv, tag - 1, error);
             if (LONG) {
                 // the new position's K/V row, when it falls in this unit
                 if (pos >= ap0 && pos < ap1)
@@ -624,7 +635,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
-            sq = take<G::DIM, false>(a.x_hidden, h_raw, tag - 1, error);
+            sq = take<G::DIM, false, false, kPollDelayC>(a.x_hidden, h_raw, tag - 1, error);
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 9 + 13 * l);
             {
@@ -648,7 +659,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
-            take<G::FFN, true>(a.x_act, xs, tag - 1, error);
+            take<G::FFN, true, false, kPollDelayD>(a.x_act, xs, tag - 1, error);
             block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {

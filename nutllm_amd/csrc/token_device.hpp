@@ -316,17 +316,23 @@ __device__ __forceinline__ float rms_scale(float squares, int n)
 }
 
 // dst[map(i)] = value of src[i] once tagged, i < N; returns this thread's
-// sum of squares. A thread's loads are issued together, and every round
+// sum of squares. The first poll waits DELAY ticks (10 ns) of the real-time
+// clock. A thread's loads are issued together, and every round
 // re-issues all of its still-stale loads together, so a late producer costs
 // one coherent round trip per round rather than one per element. Bounded:
 // gives up once any wait failed. Waits for this wave's outstanding DMA, then
 // a barrier.
-template <int N, bool SWIZZLE, bool FRESH = false>
+template <int N, bool SWIZZLE, bool FRESH = false, int DELAY = 0>
 __device__ float take(const uint64_t *src, float *dst, unsigned tag,
                       int *error)
 {
     constexpr int PER = cdiv(N, kThreads);
     const unsigned tid = FRESH ? unsigned(opaque_lane_value(threadIdx.x)) : threadIdx.x;
+    if (DELAY > 0) {
+        const unsigned long long until = __builtin_amdgcn_s_memrealtime() + DELAY;
+        while (__builtin_amdgcn_s_memrealtime() < until)
+            __builtin_amdgcn_s_sleep(1);
+    }
     uint64_t v[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++) {
