@@ -35,10 +35,16 @@ namespace {
 // producers have not written yet, and 256 workgroups doing so flood the
 // memory system with coherent reads that slow every producer's publish and
 // every consumer's later rounds. Measured per exchange (TinyLlama INT4, 16
-// tokens; 423 us per token with no delay, 388 with these): into phases A
-// (h after W2) and D (act) 450 ns, into B (q/k/v) and C (h after Wo), which
-// follow a larger weight DMA that already delays their polls, 150 ns.
-constexpr int kPollDelayA = 45, kPollDelayB = 15, kPollDelayC = 15, kPollDelayD = 45;
+// tokens: 423 us per token with no delays, 388 with these; INT8 at KV
+// 2048-2175, split attention: 602 -> 514): into phases A (h after W2) and D
+// (act) 450 ns, into B (q/k/v) and C (h after Wo), which follow a larger
+// weight DMA that already delays their polls, 150 ns; with split attention
+// 600 and 300 ns, and 900 ns for its partials and merged context.
+template <bool LONG> struct PollDelay {
+    static constexpr int A = LONG ? 60 : 45, B = LONG ? 30 : 15;
+    static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 45;
+    static constexpr int PARTIALS = 90, CONTEXT = 90;
+};
 
 template <int QT_, int DIM_, int FFN_, int HEADS_, int KVH_, int HD_, int NP_>
 struct Geo {
@@ -96,13 +102,18 @@ struct Geo {
 
 // ------------------------------------------------- split attention --
 
-// dst[i] = value of *addr(i) once tagged, i < N; as take (batched
-// re-polls, bounded), for words scattered over an exchange buffer. Ends
-// with a barrier.
-template <int N, class Addr>
+// dst[i] = value of *addr(i) once tagged, i < N; as take (a first-poll
+// delay of DELAY ticks, batched re-polls, bounded), for words scattered over
+// an exchange buffer. Ends with a barrier.
+template <int N, int DELAY, class Addr>
 __device__ void take_words(Addr addr, float *dst, unsigned tag, int *error)
 {
     constexpr int PER = cdiv(N, kThreads);
+    if (DELAY > 0) {
+        const unsigned long long until = __builtin_amdgcn_s_memrealtime() + DELAY;
+        while (__builtin_amdgcn_s_memrealtime() < until)
+            __builtin_amdgcn_s_sleep(1);
+    }
     uint64_t v[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++) {
@@ -204,7 +215,7 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
     }
     const int mh = blockIdx.x >> 3, md0 = (blockIdx.x & 7) * 8;
     const int mg = mh / G::GROUP, mhl = mh % G::GROUP;
-    take_words<G::SPLITS * 10>(
+    take_words<G::SPLITS * 10, PollDelay<true>::PARTIALS>(
         [&](int i) {
             const int sp = i / 10, j = i - sp * 10;
             return a.x_apart + size_t((mg * G::SPLITS + sp) * G::GROUP + mhl) * (G::HD + 2) +
@@ -416,7 +427,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = e.store(h_raw);
                 dma_wait();
             } else {
-                sq = take<G::DIM, false, false, kPollDelayA>(a.x_hidden, h_raw, tag - 1, error);
+                sq = take<G::DIM, false, false, PollDelay<LONG>::A>(a.x_hidden, h_raw, tag - 1, error);
             }
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 2 + 13 * l);
@@ -488,7 +499,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
-            take<G::DIM + 2 * G::KVD, false, false, kPollDelayB>(a.x_qkv, qkv, tag - 1, error);
+            take<G::DIM + 2 * G::KVD, false, false, PollDelay<LONG>::B>(a.x_qkv, qkv, tag - 1, error);
             if (LONG) {
                 // the new position's K/V row, when it falls in this unit
                 if (pos >= ap0 && pos < ap1)
@@ -512,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, tag, error);
                 tag += 2;
                 // the whole context, as digits for the Wo rows
-                take<G::DIM, false>(a.x_ctx, qkv, tag - 1, error);
+                take<G::DIM, false, false, PollDelay<true>::CONTEXT>(a.x_ctx, qkv, tag - 1, error);
                 quartet_digits<G::QT>(reinterpret_cast<const float4 *>(qkv)[threadIdx.x],
                                       threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             } else {
@@ -635,7 +646,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
-            sq = take<G::DIM, false, false, kPollDelayC>(a.x_hidden, h_raw, tag - 1, error);
+            sq = take<G::DIM, false, false, PollDelay<LONG>::C>(a.x_hidden, h_raw, tag - 1, error);
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 9 + 13 * l);
             {
@@ -659,7 +670,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
-            take<G::FFN, true, false, kPollDelayD>(a.x_act, xs, tag - 1, error);
+            take<G::FFN, true, false, PollDelay<LONG>::D>(a.x_act, xs, tag - 1, error);
             block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {
