@@ -13,6 +13,11 @@ roofline  algorithmic bytes of the decode loop (packed weights + fp16 scales
           + fp32 classifier + norms + one embedding row per token, plus K/V
           reads) / device time of the decode loop from HIP events on the
           model's stream, against the 8 TB/s HBM peak.
+          roofline.traffic: HBM bytes per generate launch measured in the same
+          run, before the timed region, by two rocprofv3 counter passes
+          (FETCH_SIZE, WRITE_SIZE) over a child run of this script, each
+          scaled by the counter's reading for a 1 GiB device-to-device copy
+          (--no-traffic skips them; traffic is then null).
 cpu_baseline  the compiled reference's own threaded generate_tokens_cached
           (oracle/_ref, "reference") or, when that library is absent, this
           repo's C restatement ("port"), timed on this host in the same run
@@ -50,12 +55,9 @@ HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16, MI355X
 PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 
-# HBM bytes one generate launch (16 iterations) moves, from rocprofv3
-# counter runs of this bench (profiles/token_kernel_tinyllama_int4_decode.md):
-# FETCH_SIZE x 1.99993 + WRITE_SIZE x 1.0 KiB, the scales read off a 1 GiB
-# device-to-device copy in the same runs.
-MEASURED_TRAFFIC_BYTES = 13_535_409_278
 CPU_SAMPLE_SECONDS = 8.0
+TRAFFIC_PASS_TIMEOUT = 180  # seconds per rocprofv3 counter pass
+CALIBRATE_MIB = 1024
 MAX_THREADS = 16  # the GPU box's CPU share
 
 
@@ -87,6 +89,68 @@ def cpu_info():
         cores.add((phys, core))
     n = len(cores) or (os.cpu_count() or 1)
     return model, n
+
+
+def counter_pass(counter):
+    """One rocprofv3 counter pass over a single generate of this workload
+    (a child process: python3 bench.py under rocprofv3 --pmc COUNTER), plus
+    a CALIBRATE_MIB device-to-device copy in the same process. Returns
+    (KiB per token-kernel dispatch, KiB per copy dispatch)."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import tempfile
+    tool = shutil.which("rocprofv3")
+    if tool is None:
+        raise RuntimeError("rocprofv3 not found")
+    out = tempfile.mkdtemp(prefix="nut_pmc_")
+    cmd = [tool, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--",
+           sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic",
+           "--steps", "1", "--warmup", "0", "--calibrate-copy-mib", str(CALIBRATE_MIB)]
+    proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                            start_new_session=True)
+    try:
+        proc.wait(timeout=TRAFFIC_PASS_TIMEOUT)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.wait()
+        raise RuntimeError(f"{counter} pass timed out")
+    # (the tool can end with SIGSEGV in exit() after writing complete files)
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    kernel, copy = [], []
+    for name in files:
+        with open(name, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                v = float(row["Counter_Value"])
+                k = row.get("Kernel_Name", "")
+                if "token_kernel" in k:
+                    kernel.append(v)
+                elif "copyBuffer" in k:
+                    copy.append(v)
+    shutil.rmtree(out, ignore_errors=True)
+    if not kernel or not copy:
+        raise RuntimeError(f"{counter} pass: no token-kernel or copy dispatch "
+                           f"(exit status {proc.returncode})")
+    # the calibration copies are the largest copy dispatches (model upload
+    # copies are small)
+    return statistics.mean(kernel), max(copy)
+
+
+def measured_traffic():
+    """HBM bytes of one generate launch (16 iterations) from FETCH_SIZE and
+    WRITE_SIZE counter passes of this build, each scaled by what the counter
+    reads for the CALIBRATE_MIB copy: FETCH_SIZE counts half of a copy's read
+    bytes on this GPU, WRITE_SIZE all of its written bytes."""
+    true_kib = CALIBRATE_MIB * 1024
+    fetch, fetch_copy = counter_pass("FETCH_SIZE")
+    write, write_copy = counter_pass("WRITE_SIZE")
+    f_scale, w_scale = true_kib / fetch_copy, true_kib / write_copy
+    return {"bytes": int(round((fetch * f_scale + write * w_scale) * 1024)),
+            "fetch_kib": round(fetch, 1), "fetch_scale": round(f_scale, 5),
+            "write_kib": round(write, 1), "write_scale": round(w_scale, 5)}
 
 
 def kv_bytes_per_position(cfg):
@@ -332,6 +396,9 @@ def main():
                     help="steps: eager per-token step kernels only (no token "
                          "kernel, batched prefill or graph replay), for "
                          "profiling the step kernels")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure "
+                         "roofline.traffic")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the timed region, copy this many MiB device "
                          "to device (the known-size kernel that scales "
@@ -341,6 +408,17 @@ def main():
         print("bench.py measures one GPU: nutllm_amd has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+
+    # The counter passes run as child processes before this process touches
+    # the GPU (default workload only).
+    traffic, traffic_error = None, None
+    if args.workload == "tinyllama_int4" and not args.no_traffic:
+        log("measuring HBM traffic (two rocprofv3 counter passes)")
+        try:
+            traffic = measured_traffic()
+        except (RuntimeError, OSError, ValueError, KeyError) as e:
+            traffic_error = str(e)
+            log(f"traffic not measured: {e}")
 
     import nutllm_amd as nut
     from nutllm_amd import workloads
@@ -413,12 +491,17 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": MEASURED_TRAFFIC_BYTES,
+            "traffic": None if traffic is None else traffic["bytes"],
             "kernel": "decode loop (classifier + argmax + decode step per "
                       "token)",
             "bytes_per_launch": step_bytes,
         },
     }
+    if traffic is not None:
+        line["roofline"]["traffic_ratio"] = round(traffic["bytes"] / step_bytes, 4)
+        line["roofline"]["traffic_counters"] = traffic
+    elif traffic_error is not None:
+        line["roofline"]["traffic_error"] = traffic_error
     if args.calibrate_copy_mib > 0:
         nbytes = args.calibrate_copy_mib << 20
         src, dst = nut.DeviceArray(nbytes), nut.DeviceArray(nbytes)
