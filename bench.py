@@ -96,7 +96,6 @@ def counter_pass(counter):
     (a child process: python3 bench.py under rocprofv3 --pmc COUNTER), plus
     a CALIBRATE_MIB device-to-device copy in the same process. Returns
     (KiB per token-kernel dispatch, KiB per copy dispatch)."""
-    import csv
     import glob
     import shutil
     import signal
@@ -118,25 +117,37 @@ def counter_pass(counter):
         raise RuntimeError(f"{counter} pass timed out")
     # (the tool can end with SIGSEGV in exit() after writing complete files)
     files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
-    kernel, copy = [], []
+    try:
+        return parse_counter_csv(files, counter)
+    except RuntimeError as e:
+        raise RuntimeError(f"{e} (exit status {proc.returncode})") from None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def parse_counter_csv(files, counter):
+    """(mean value per token-kernel dispatch, value of the largest copy
+    dispatch) of `counter` in rocprofv3 counter-collection CSV files. A
+    dispatch's rows (one per counter in the files seen here) are summed."""
+    import csv
+    kernel, copy = {}, {}
     for name in files:
         with open(name, newline="") as f:
             for row in csv.DictReader(f):
                 if row.get("Counter_Name") != counter:
                     continue
+                key = (name, row.get("Dispatch_Id", ""))
                 v = float(row["Counter_Value"])
                 k = row.get("Kernel_Name", "")
                 if "token_kernel" in k:
-                    kernel.append(v)
+                    kernel[key] = kernel.get(key, 0.0) + v
                 elif "copyBuffer" in k:
-                    copy.append(v)
-    shutil.rmtree(out, ignore_errors=True)
+                    copy[key] = copy.get(key, 0.0) + v
     if not kernel or not copy:
-        raise RuntimeError(f"{counter} pass: no token-kernel or copy dispatch "
-                           f"(exit status {proc.returncode})")
+        raise RuntimeError(f"{counter} pass: no token-kernel or copy dispatch")
     # the calibration copies are the largest copy dispatches (model upload
     # copies are small)
-    return statistics.mean(kernel), max(copy)
+    return statistics.mean(kernel.values()), max(copy.values())
 
 
 def measured_traffic():

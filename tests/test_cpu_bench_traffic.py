@@ -1,0 +1,50 @@
+"""bench.py's HBM-traffic measurement: parsing of rocprofv3 counter files
+(the counter passes themselves need a GPU; the driver's bench run makes
+them)."""
+import importlib.util
+import os
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = ("Correlation_Id,Dispatch_Id,Agent_Id,Queue_Id,Process_Id,Thread_Id,Grid_Size,"
+          "Kernel_Id,Kernel_Name,Workgroup_Size,LDS_Block_Size,Scratch_Size,VGPR_Count,"
+          "Accum_VGPR_Count,SGPR_Count,Counter_Name,Counter_Value,Start_Timestamp,"
+          "End_Timestamp")
+
+
+def bench():
+    spec = importlib.util.spec_from_file_location("bench", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def row(dispatch, kernel, counter, value):
+    return (f'{dispatch},{dispatch},1,1,1,1,131072,{dispatch},"{kernel}",512,0,0,0,0,0,'
+            f'{counter},{value},0,1')
+
+
+def test_parse_counter_csv(tmp_path):
+    b = bench()
+    k = "void nut::(anonymous namespace)::token_kernel<Geo<1, 2048>, true, false>(nut::TokenArgs)"
+    lines = [HEADER,
+             row(1, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 12.0),  # upload copy
+             row(2, k, "FETCH_SIZE", 4000.0), row(2, k, "FETCH_SIZE", 500.0),  # two XCD rows
+             row(3, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 524288.0),
+             row(4, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 524290.0),
+             row(5, "qkv_fast_kernel<1, 2>", "FETCH_SIZE", 99.0),
+             row(6, k, "WRITE_SIZE", 7.0)]
+    f = tmp_path / "run_counter_collection.csv"
+    f.write_text("\n".join(lines) + "\n")
+    kernel, copy = b.parse_counter_csv([str(f)], "FETCH_SIZE")
+    assert kernel == pytest.approx(4500.0)  # rows of one dispatch summed
+    assert copy == pytest.approx(524290.0)  # the largest copy dispatch
+
+
+def test_parse_counter_csv_missing(tmp_path):
+    b = bench()
+    f = tmp_path / "run_counter_collection.csv"
+    f.write_text(HEADER + "\n" + row(1, "qkv_fast_kernel<1, 2>", "FETCH_SIZE", 1.0) + "\n")
+    with pytest.raises(RuntimeError):
+        b.parse_counter_csv([str(f)], "FETCH_SIZE")
