@@ -24,6 +24,16 @@ __device__ __forceinline__ uint4 load_stream(const uint8_t *p)
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A weight chunk: nontemporal (STREAM, every byte read once) or through the
+// caches (rows that other workgroups of the XCD read again).
+template <bool STREAM>
+__device__ __forceinline__ uint4 load_chunk(const uint8_t *p)
+{
+    if (STREAM)
+        return load_stream(p);
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
 // Pointers of rows row0 .. row0 + n - 1 of m (rows past the end re-read the
 // last row) into slots base .. base + n - 1.
 template <int QT, int R>
@@ -59,8 +69,9 @@ template <int QT> inline size_t staged_x_bytes(int cols)
 // every lane gets all sums. Every wave of the workgroup calls it (`active`
 // false for waves without rows): the workgroup stages x' once into LDS (xs,
 // staged_x_bytes) and reduces sum x^2 in red[kRowWaves]; each wave issues its
-// first weight chunks before the staging, so they load meanwhile.
-template <int QT, int R, bool NORM>
+// first weight chunks before the staging, so they load meanwhile. STREAM:
+// the weight loads' cache policy (load_chunk).
+template <int QT, int R, bool NORM, bool STREAM = true>
 __device__ __forceinline__ void rows_matvec(const uint8_t *const (&rp)[R],
                                             const uint16_t *const (&sp)[R], int cols,
                                             const float *x, const float *nw, bool active,
@@ -76,7 +87,7 @@ __device__ __forceinline__ void rows_matvec(const uint8_t *const (&rp)[R],
     if (first) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            w0[r] = load_stream(rp[r] + 16 * lane);
+            w0[r] = load_chunk<STREAM>(rp[r] + 16 * lane);
             s0[r] = half_bits_to_float(sp[r][QT == 1 ? lane : lane >> 1]);
         }
     }
@@ -143,7 +154,7 @@ __device__ __forceinline__ void rows_matvec(const uint8_t *const (&rp)[R],
             float s[R];
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                w[r] = load_stream(rp[r] + 16 * c);
+                w[r] = load_chunk<STREAM>(rp[r] + 16 * c);
                 s[r] = half_bits_to_float(sp[r][QT == 1 ? c : c >> 1]);
             }
             chunk(c, w, s);

@@ -39,30 +39,53 @@ constexpr int kAttnChunk = 32;    // positions per attention chunk (8 per wave)
 constexpr int kAttnMaxSplits = 32;
 constexpr int kDppRowRor8 = 0x128; // row_ror:8, lane i <- lane i ^ 8 in a row
 
-__device__ __forceinline__ int wave_id()
+__device__ __forceinline__ int wave_id(int block)
 {
-    return __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + threadIdx.x / kWave);
+    return __builtin_amdgcn_readfirstlane(block * kWaves + threadIdx.x / kWave);
+}
+
+// Workgroups go to the 8 XCDs round-robin (blockIdx % 8 is the XCD).
+constexpr int kXcds = 8;
+
+// The (row block, token) of this workgroup. Decode (CHUNK false): block
+// blockIdx.x, token blockIdx.y. Prompt chunks: a flat grid of
+// ceil(blocks / 8) * 8 * tokens workgroups in which the chunk's tokens of
+// row block b are consecutive workgroups on b's XCD, so that the weight rows
+// one of them reads come from that XCD's L2 for the others. Returns false
+// for the padding workgroups (block >= blocks).
+template <bool CHUNK>
+__device__ __forceinline__ bool chunk_cell(int blocks, int tokens, int &block, int &t)
+{
+    if (!CHUNK) {
+        block = blockIdx.x;
+        t = blockIdx.y;
+        return true;
+    }
+    const int i = blockIdx.x, rest = i / kXcds;
+    t = rest % tokens;
+    block = (rest / tokens) * kXcds + i % kXcds;
+    return block < blocks;
 }
 
 // Q/K/V rows of rmsnorm(h) * attention_norm (concatenated: query rows, key
 // rows, value rows; R divides dim and kv_heads * head_dim), RoPE on the
 // query and key pairs at position *length (src/quant_model.cpp:26-37), key
 // and value rows into the layer's cache.
-template <int QT, int R>
+template <int QT, int R, bool CHUNK = false>
 __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
     DecodeShape s, const float *hidden, const float *norm, QMat wq, QMat wk,
     QMat wv, const float2 *rope, const int *length, float *k_layer,
-    float *v_layer, float *query, const StepState *state)
+    float *v_layer, float *query, int blocks, int tokens, const StepState *state)
 {
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
-    if (state->done)
+    int block, t;
+    if (state->done || !chunk_cell<CHUNK>(blocks, tokens, block, t))
         return;
-    const int t = blockIdx.y;
     hidden += size_t(t) * s.dim;
     query += size_t(t) * s.dim;
     const int kvd = s.kv_heads * s.head_dim;
-    const int row = wave_id() * R;
+    const int row = wave_id(block) * R;
     const bool active = row < s.dim + 2 * kvd;
     const int which = row < s.dim ? 0 : row < s.dim + kvd ? 1 : 2;
     const int local = which == 0 ? row : which == 1 ? row - s.dim : row - s.dim - kvd;
@@ -70,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
     const uint16_t *sp[R];
     row_ptrs<QT, R>(which == 0 ? wq : which == 1 ? wk : wv, local, 0, R, rp, sp);
     float out[R];
-    rows_matvec<QT, R, true>(rp, sp, s.dim, hidden, norm, active, xs, red, out);
+    rows_matvec<QT, R, true, !CHUNK>(rp, sp, s.dim, hidden, norm, active, xs, red, out);
     if (!active)
         return;
     const int pos = *length + t;
@@ -95,21 +118,23 @@ __global__ __launch_bounds__(kThreads) void qkv_fast_kernel(
 }
 
 // y[r] += (W x)[r]  (Wo + residual, W2 + residual)
-template <int QT, int R>
+template <int QT, int R, bool CHUNK = false>
 __global__ __launch_bounds__(kThreads) void residual_fast_kernel(
-    QMat m, const float *x, float *y, const StepState *state)
+    QMat m, const float *x, float *y, int blocks, int tokens, const StepState *state)
 {
     extern __shared__ float xs[];
-    if (state->done)
+    int block, t;
+    if (state->done || !chunk_cell<CHUNK>(blocks, tokens, block, t))
         return;
-    x += size_t(blockIdx.y) * m.cols;
-    y += size_t(blockIdx.y) * m.rows;
-    const int row = wave_id() * R;
+    x += size_t(t) * m.cols;
+    y += size_t(t) * m.rows;
+    const int row = wave_id(block) * R;
     const uint8_t *rp[R];
     const uint16_t *sp[R];
     row_ptrs<QT, R>(m, row, 0, R, rp, sp);
     float out[R];
-    rows_matvec<QT, R, false>(rp, sp, m.cols, x, nullptr, row < m.rows, xs, nullptr, out);
+    rows_matvec<QT, R, false, !CHUNK>(rp, sp, m.cols, x, nullptr, row < m.rows, xs, nullptr,
+                                      out);
     if (row < m.rows && (threadIdx.x & (kWave - 1)) == 0)
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -119,24 +144,26 @@ __global__ __launch_bounds__(kThreads) void residual_fast_kernel(
 
 // act[r] = silu((Wg xn)[r]) * (Wu xn)[r], xn = rmsnorm(h) * ffn_norm
 // (src/quant_model.cpp:194-198); R rows of each matrix per wave.
-template <int QT, int R>
+template <int QT, int R, bool CHUNK = false>
 __global__ __launch_bounds__(kThreads) void gate_up_fast_kernel(
-    const float *hidden, const float *norm, QMat wg, QMat wu, float *act,
-    const StepState *state)
+    const float *hidden, const float *norm, QMat wg, QMat wu, float *act, int blocks,
+    int tokens, const StepState *state)
 {
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
-    if (state->done)
+    int block, t;
+    if (state->done || !chunk_cell<CHUNK>(blocks, tokens, block, t))
         return;
-    hidden += size_t(blockIdx.y) * wg.cols;
-    act += size_t(blockIdx.y) * wg.rows;
-    const int row = wave_id() * R;
+    hidden += size_t(t) * wg.cols;
+    act += size_t(t) * wg.rows;
+    const int row = wave_id(block) * R;
     const uint8_t *rp[2 * R];
     const uint16_t *sp[2 * R];
     row_ptrs<QT, 2 * R>(wg, row, 0, R, rp, sp);
     row_ptrs<QT, 2 * R>(wu, row, R, R, rp, sp);
     float gu[2 * R];
-    rows_matvec<QT, 2 * R, true>(rp, sp, wg.cols, hidden, norm, row < wg.rows, xs, red, gu);
+    rows_matvec<QT, 2 * R, true, !CHUNK>(rp, sp, wg.cols, hidden, norm, row < wg.rows, xs, red,
+                                         gu);
     if (row < wg.rows && (threadIdx.x & (kWave - 1)) == 0)
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -553,8 +580,20 @@ void launch_attention_g(const DecodeShape &s, const float *k_layer, const float 
     launch_attention<HD, 1>(s, k_layer, v_layer, length, b, tokens, state, stream);
 }
 
-template <int QT, int HD>
-void launch_layer_fast_t(const DecodeShape &s, const LayerView &w,
+// Grid of a row kernel over `blocks` row blocks and `tokens` tokens, in the
+// layout chunk_cell<CHUNK> reads.
+dim3 row_grid(int blocks, int tokens, bool chunk)
+{
+    if (!chunk)
+        return dim3(blocks, tokens);
+    return dim3(((blocks + kXcds - 1) / kXcds) * kXcds * tokens);
+}
+
+// One layer on the step kernels. CHUNK: a prompt chunk of several tokens,
+// whose workgroups of one row block share an XCD and read the weights
+// through the caches; otherwise one token, weights streamed.
+template <int QT, int HD, bool CHUNK>
+void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
                          const float2 *rope, const int *length, float *k_layer,
                          float *v_layer, const StepBuffers &b, int tokens,
                          const StepState *state, hipStream_t stream)
@@ -563,30 +602,53 @@ void launch_layer_fast_t(const DecodeShape &s, const LayerView &w,
     const size_t x_dim = staged_x_bytes<QT>(s.dim), x_ffn = staged_x_bytes<QT>(s.ffn_dim);
     const int qkv_rows = s.dim + 2 * kvd;
     // four rows per wave where that still gives every CU a workgroup
-    if (qkv_rows >= 8192 && s.dim % 4 == 0 && kvd % 4 == 0)
-        hipLaunchKernelGGL((qkv_fast_kernel<QT, 4>), dim3(blocks_for_rows(qkv_rows, 4), tokens),
+    if (qkv_rows >= 8192 && s.dim % 4 == 0 && kvd % 4 == 0) {
+        const int blocks = blocks_for_rows(qkv_rows, 4);
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 4, CHUNK>), row_grid(blocks, tokens, CHUNK),
                            dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
                            w.query, w.key, w.value, rope, length, k_layer, v_layer,
-                           b.query, state);
-    else
-        hipLaunchKernelGGL((qkv_fast_kernel<QT, 2>), dim3(blocks_for_rows(qkv_rows, 2), tokens),
+                           b.query, blocks, tokens, state);
+    } else {
+        const int blocks = blocks_for_rows(qkv_rows, 2);
+        hipLaunchKernelGGL((qkv_fast_kernel<QT, 2, CHUNK>), row_grid(blocks, tokens, CHUNK),
                            dim3(kThreads), x_dim, stream, s, b.hidden, w.attention_norm,
                            w.query, w.key, w.value, rope, length, k_layer, v_layer,
-                           b.query, state);
+                           b.query, blocks, tokens, state);
+    }
     launch_attention_g<HD>(s, k_layer, v_layer, length, b, tokens, state, stream);
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2), tokens),
-                       dim3(kThreads), x_dim, stream, w.output, b.context, b.hidden, state);
-    if (s.ffn_dim >= 8192)
-        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4>),
-                           dim3(blocks_for_rows(s.ffn_dim, 4), tokens), dim3(kThreads), x_dim,
-                           stream, b.hidden, w.ffn_norm, w.gate, w.up, b.act, state);
-    else
-        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 2>),
-                           dim3(blocks_for_rows(s.ffn_dim, 2), tokens), dim3(kThreads), x_dim,
-                           stream, b.hidden, w.ffn_norm, w.gate, w.up, b.act, state);
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2>), dim3(blocks_for_rows(s.dim, 2), tokens),
-                       dim3(kThreads), x_ffn, stream, w.down, b.act, b.hidden, state);
+    const int dim_blocks = blocks_for_rows(s.dim, 2);
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2, CHUNK>), row_grid(dim_blocks, tokens, CHUNK),
+                       dim3(kThreads), x_dim, stream, w.output, b.context, b.hidden, dim_blocks,
+                       tokens, state);
+    if (s.ffn_dim >= 8192) {
+        const int blocks = blocks_for_rows(s.ffn_dim, 4);
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4, CHUNK>), row_grid(blocks, tokens, CHUNK),
+                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate, w.up,
+                           b.act, blocks, tokens, state);
+    } else {
+        const int blocks = blocks_for_rows(s.ffn_dim, 2);
+        hipLaunchKernelGGL((gate_up_fast_kernel<QT, 2, CHUNK>), row_grid(blocks, tokens, CHUNK),
+                           dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate, w.up,
+                           b.act, blocks, tokens, state);
+    }
+    hipLaunchKernelGGL((residual_fast_kernel<QT, 2, CHUNK>), row_grid(dim_blocks, tokens, CHUNK),
+                       dim3(kThreads), x_ffn, stream, w.down, b.act, b.hidden, dim_blocks,
+                       tokens, state);
     check_launch("decode step");
+}
+
+template <int QT, int HD>
+void launch_layer_fast_t(const DecodeShape &s, const LayerView &w,
+                         const float2 *rope, const int *length, float *k_layer,
+                         float *v_layer, const StepBuffers &b, int tokens,
+                         const StepState *state, hipStream_t stream)
+{
+    if (tokens > 1)
+        launch_layer_fast_c<QT, HD, true>(s, w, rope, length, k_layer, v_layer, b, tokens,
+                                          state, stream);
+    else
+        launch_layer_fast_c<QT, HD, false>(s, w, rope, length, k_layer, v_layer, b, tokens,
+                                           state, stream);
 }
 
 } // namespace
