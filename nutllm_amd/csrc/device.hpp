@@ -51,6 +51,31 @@ __device__ __forceinline__ float dpp(float v, float fill)
         __float_as_int(fill), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
 }
 
+// a0 += q_J · k0 and a1 += q_{J+1} · k1, component by component (x, y, z,
+// w; a0 then a1 each time, so the rounding is that of the fmaf chain in
+// this order), where q_j is the float4 q of lane j of this lane's row of 16
+// lanes, read by v_fmac_f32 through a row_newbcast DPP source. Every lane
+// of the row must be active. The s_nop covers a VALU write of q just
+// before (DPP reads need two wait states after one).
+template <int J>
+__device__ __forceinline__ void fma_row_bcast2(float &a0, float &a1, float4 q, float4 k0,
+                                               float4 k1)
+{
+    static_assert(J >= 0 && J + 1 < 16, "lanes of a 16-lane row");
+    asm volatile("s_nop 1\n\t"
+                 "v_fmac_f32_dpp %0, %2, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %1, %2, %10 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %3, %7 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %1, %3, %11 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %1, %4, %12 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %0, %5, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_fmac_f32_dpp %1, %5, %13 row_newbcast:%15 row_mask:0xf bank_mask:0xf"
+                 : "+v"(a0), "+v"(a1)
+                 : "v"(q.x), "v"(q.y), "v"(q.z), "v"(q.w), "v"(k0.x), "v"(k0.y), "v"(k0.z),
+                   "v"(k0.w), "v"(k1.x), "v"(k1.y), "v"(k1.z), "v"(k1.w), "i"(J), "i"(J + 1));
+}
+
 // Sum over each row of 16 lanes, in every lane of the row.
 __device__ __forceinline__ float row16_sum(float v)
 {

@@ -536,7 +536,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 const int g = (wave * G::HPW) / G::GROUP;
                 const float *kg = kst + g * n * G::KROW;
                 const float *vg = vst + g * n * G::KROW;
-                const float4 *q4 = reinterpret_cast<const float4 *>(qkv + head * G::HD);
+                // lane r holds dims 4r..4r+3 of q; each product takes dims
+                // 4j..4j+3 from lane j of the row by DPP broadcast (no LDS
+                // reads of q), so every lane of the wave runs the dot, a
+                // lane past n on the last row's K
+                const float4 qv = reinterpret_cast<const float4 *>(qkv + head * G::HD)[r];
                 float *sc = scores + head * G::NP;
                 float s[PASSES];
                 float m = -INFINITY;
@@ -545,25 +549,19 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     s[ps] = -INFINITY;
                     if (ps * 16 < n) {
                         const int p = ps * 16 + r;
-                        if (p < n) {
-                            const float4 *k4 =
-                                reinterpret_cast<const float4 *>(kg + p * G::KROW);
-                            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-                            for (int d4 = 0; d4 < 16; d4 += 2) {
-                                const float4 k0 = k4[d4], q0 = q4[d4];
-                                const float4 k1 = k4[d4 + 1], q1 = q4[d4 + 1];
-                                a0 = fmaf(q0.x, k0.x, a0);
-                                a1 = fmaf(q1.x, k1.x, a1);
-                                a0 = fmaf(q0.y, k0.y, a0);
-                                a1 = fmaf(q1.y, k1.y, a1);
-                                a0 = fmaf(q0.z, k0.z, a0);
-                                a1 = fmaf(q1.z, k1.z, a1);
-                                a0 = fmaf(q0.w, k0.w, a0);
-                                a1 = fmaf(q1.w, k1.w, a1);
-                            }
+                        const float4 *k4 =
+                            reinterpret_cast<const float4 *>(kg + min(p, n - 1) * G::KROW);
+                        float a0 = 0.0f, a1 = 0.0f;
+                        fma_row_bcast2<0>(a0, a1, qv, k4[0], k4[1]);
+                        fma_row_bcast2<2>(a0, a1, qv, k4[2], k4[3]);
+                        fma_row_bcast2<4>(a0, a1, qv, k4[4], k4[5]);
+                        fma_row_bcast2<6>(a0, a1, qv, k4[6], k4[7]);
+                        fma_row_bcast2<8>(a0, a1, qv, k4[8], k4[9]);
+                        fma_row_bcast2<10>(a0, a1, qv, k4[10], k4[11]);
+                        fma_row_bcast2<12>(a0, a1, qv, k4[12], k4[13]);
+                        fma_row_bcast2<14>(a0, a1, qv, k4[14], k4[15]);
+                        if (p < n)
                             s[ps] = (a0 + a1) * a.attn_scale;
-                        }
                         m = fmaxf(m, s[ps]);
                     }
                 }
