@@ -10,9 +10,14 @@ resident in HBM before the timed region.
 value     decode tok/s with the reference's GenerationStats semantics
           (every classifier + argmax + decode step after the prefill).
 roofline  algorithmic bytes of the decode loop (packed weights + fp16 scales
-          + fp32 classifier + norms + one embedding row per token, plus K/V
-          reads) / device time of the decode loop from HIP events on the
-          model's stream, against the 8 TB/s HBM peak.
+          + the classifier's fp16 screening copy and row bounds + norms + one
+          embedding row per token, plus K/V reads) / device time of the
+          decode loop from HIP events on the model's stream, against the
+          8 TB/s HBM peak. The argmax reads the fp32 classifier rows only
+          for the few rows the fp16 copy's error bounds cannot rule out
+          (not counted).
+model_weight_roofline  the same with the model's own weight bytes (the
+          fp32 classifier as stored): weight bytes per token / step time.
           roofline.traffic: HBM bytes per generate launch measured in the same
           run, before the timed region, by two rocprofv3 counter passes
           (FETCH_SIZE, WRITE_SIZE) over a child run of this script, each
@@ -274,8 +279,11 @@ def long_prompt(args, nut, workloads):
     device_ms = statistics.median(dms)
     per_pos = kv_bytes_per_position(cfg)
     kv_bytes = sum(per_pos * (len(prompt) + i + 1) for i in range(n))
-    step_bytes = model.weight_bytes_per_token() * n + kv_bytes
+    screened = args.path != "steps"  # the token kernels screen the classifier
+    step_bytes = model.weight_bytes_per_token(screened=screened) * n + kv_bytes
+    model_bytes = model.weight_bytes_per_token() * n + kv_bytes
     achieved = step_bytes / (device_ms * 1e-3) / 1e9
+    model_achieved = model_bytes / (device_ms * 1e-3) / 1e9
     line = {
         "metric": f"decode tok/s, {args.workload} (greedy, {len(prompt)}-token prompt, "
                   f"{gen} tokens)",
@@ -295,6 +303,9 @@ def long_prompt(args, nut, workloads):
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None, "kernel": "decode loop (classifier + argmax + "
                      "decode step per token)", "bytes_per_launch": step_bytes},
+        "model_weight_roofline": {"achieved": round(model_achieved, 1), "unit": "GB/s",
+                                  "frac": round(model_achieved / HBM_PEAK_GBS, 4),
+                                  "bytes_per_launch": model_bytes},
         "prefill_tok_s": round(len(prompt) / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
         "prefill_roofline": {"bound": "mfma", "achieved": round(flop / prefill_s / 1e12, 1),
@@ -470,8 +481,10 @@ def main():
     per_pos = kv_bytes_per_position(cfg)
     # each decode-loop iteration at cache length P+i reads K/V of P+i+1
     kv_bytes = sum(per_pos * (len(prompt) + i + 1) for i in range(n))
-    step_bytes = model.weight_bytes_per_token() * n + kv_bytes
+    step_bytes = model.weight_bytes_per_token(screened=True) * n + kv_bytes
+    model_bytes = model.weight_bytes_per_token() * n + kv_bytes
     achieved = step_bytes / (statistics.median(device_ms) * 1e-3) / 1e9
+    model_achieved = model_bytes / (statistics.median(device_ms) * 1e-3) / 1e9
     line = {
         "metric": "decode tok/s, TinyLlama-1.1B-shape INT4 (greedy, 5-token "
                   "prompt, 16 tokens)",
@@ -506,6 +519,11 @@ def main():
             "kernel": "decode loop (classifier + argmax + decode step per "
                       "token)",
             "bytes_per_launch": step_bytes,
+        },
+        "model_weight_roofline": {
+            "achieved": round(model_achieved, 1), "unit": "GB/s",
+            "frac": round(model_achieved / HBM_PEAK_GBS, 4),
+            "bytes_per_launch": model_bytes,
         },
     }
     if traffic is not None:

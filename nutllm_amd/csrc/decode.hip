@@ -374,6 +374,63 @@ __global__ __launch_bounds__(kThreads) void pick_token_kernel(
     }
 }
 
+// The screening copy of the fp32 classifier, one wave per row j: the row
+// times 2^e_j in fp16 (round to nearest; e_j puts the row's largest
+// magnitude in [2^14, 2^15), at most 2^100) and screen[j] = (c_j, 2^-e_j),
+// where c_j bounds |s_j - a_j| / ||x||_2 for any fp32 input x: s_j is the
+// fp32 logit (any summation order of fp32 FMAs), a_j the same sum over the
+// fp16 copy times 2^-e_j. With n = dim, u16 = 2^-11 and gamma = n 2^-24 /
+// (1 - n 2^-24): the copy's error is at most u16 |w| + 2^-14-e_j per weight
+// (2^-14: a flushed subnormal), each sum's rounding at most gamma times its
+// sum of absolute terms, so
+//   c_j = 1.01 (||w_j|| (u16 + gamma (2 + u16)) + 2^-14-e_j sqrt(n) (1 + gamma)),
+// the 1 % covering the fp32 rounding of the norm of x and of the bound
+// itself. A row with a non-finite weight gets c_j = infinity.
+__global__ __launch_bounds__(kThreads) void classifier_screen_kernel(
+    const float *w, int vocab, int dim, uint16_t *w16, float2 *screen)
+{
+    const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (row >= vocab)
+        return;
+    const float *r = w + size_t(row) * dim;
+    double ss = 0.0;
+    float mx = 0.0f;
+    bool finite = true;
+    for (int i = lane; i < dim; i += kWave) {
+        const float v = r[i];
+        finite = finite && isfinite(v);
+        mx = fmaxf(mx, fabsf(v));
+        ss = fma(double(v), double(v), ss);
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        ss += __shfl_xor(ss, off);
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    finite = __all(finite);
+    int e = 0;
+    if (finite && mx > 0.0f) {
+        int k;
+        (void)frexpf(mx, &k); // mx = m 2^k, m in [0.5, 1)
+        e = min(15 - k, 100);
+    }
+    uint16_t *d = w16 + size_t(row) * dim;
+    for (int i = lane; i < dim; i += kWave)
+        d[i] = __builtin_bit_cast(uint16_t, _Float16(finite ? ldexpf(r[i], e) : 0.0f));
+    if (lane == 0) {
+        float c = INFINITY;
+        if (finite) {
+            const double n = dim, u16 = 0x1p-11;
+            const double gamma = n * 0x1p-24 / (1.0 - n * 0x1p-24);
+            const double bound =
+                1.01 * (sqrt(ss) * (u16 + gamma * (2.0 + u16)) +
+                        ldexp(1.0, -14 - e) * sqrt(n) * (1.0 + gamma));
+            c = float(bound * (1.0 + 0x1p-20)); // not below the double value
+        }
+        screen[row] = make_float2(c, ldexpf(1.0f, -e));
+    }
+}
+
 __global__ void set_int_kernel(int *target, int value) { *target = value; }
 
 __global__ void reset_state_kernel(StepState *state, int token)
@@ -476,6 +533,14 @@ void launch_classifier(const DecodeShape &s, const float *hidden,
                        dim3(kThreads), lds, stream, s, hidden, final_norm,
                        weights, logits, part_val, part_idx, state);
     check_launch("generation: classifier");
+}
+
+void launch_classifier_screen(const float *weights, int vocab, int dim, uint16_t *w16,
+                              float2 *screen, hipStream_t stream)
+{
+    hipLaunchKernelGGL(classifier_screen_kernel, dim3((vocab + kWaves - 1) / kWaves),
+                       dim3(kThreads), 0, stream, weights, vocab, dim, w16, screen);
+    check_launch("classifier screening copy");
 }
 
 void launch_set_int(int *target, int value, hipStream_t stream)

@@ -341,6 +341,7 @@ void set_globals(nut_model &m, const float *embeddings,
     if (!m.tied)
         upload(m.lm_head.get(), lm_head, vocab * dim * sizeof(float));
     m.globals_set = true;
+    m.screen_ready = false;
 }
 
 void set_layer(nut_model &m, size_t layer, const nut_qmatrix *const mats[7],
@@ -510,6 +511,30 @@ bool use_token_kernel(nut_model &m, size_t end_length)
     return ok;
 }
 
+// The classifier's screening copy (launch_classifier_screen) for the
+// generate loop, when the vocabulary's share per workgroup fits the
+// kernel's bound array; null otherwise.
+void prepare_screen(nut_model &m, const uint16_t *&w16, const float2 *&screen)
+{
+    w16 = nullptr;
+    screen = nullptr;
+    const int vocab = m.shape.vocab, dim = m.shape.dim;
+    if ((vocab + kTokenGrid - 1) / kTokenGrid > kScreenRowsMax)
+        return;
+    if (!m.screen_ready) {
+        if (m.classifier16.get() == nullptr) {
+            m.classifier16.allocate(size_t(vocab) * dim * sizeof(uint16_t));
+            m.classifier_screen.allocate(size_t(vocab) * sizeof(float2));
+        }
+        launch_classifier_screen(m.output_weights(), vocab, dim,
+                                 m.classifier16.as<uint16_t>(),
+                                 m.classifier_screen.as<float2>(), m.stream);
+        m.screen_ready = true;
+    }
+    w16 = m.classifier16.as<uint16_t>();
+    screen = m.classifier_screen.as<float2>();
+}
+
 void prepare_token_kernel(nut_model &m)
 {
     if (m.exchange.get() == nullptr) {
@@ -534,6 +559,8 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.embeddings = m.embeddings.as<float>();
     a.final_norm = m.final_norm.as<float>();
     a.classifier = m.output_weights();
+    if (classify)
+        prepare_screen(m, a.classifier16, a.classifier_screen);
     a.rope = m.rope.as<float2>();
     a.k_cache = kv.keys.as<float>();
     a.v_cache = kv.values.as<float>();

@@ -250,6 +250,8 @@ template <class G> struct Lds {
     static constexpr int TOTAL = MISC + 16;
     static constexpr size_t BYTES = size_t(TOTAL) * sizeof(float);
     static_assert(BYTES <= 160 * 1024, "LDS budget");
+    static_assert(kWaves * G::HPW * G::NP >= kScreenRowsMax,
+                  "the screened classifier's upper bounds fit the scores region");
 };
 
 // CLASSIFY: the generate loop (classifier + argmax first in every
@@ -381,7 +383,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             __syncthreads();
             float best_v;
             int best_i;
-            classifier_best<G::DIM>(wcls, xs, a.vocab, best_v, best_i);
+            if (a.classifier16 != nullptr)
+                classifier_screened<G::DIM>(wcls, a.classifier16, a.classifier_screen, xs,
+                                            a.vocab, scores, red, best_v, best_i);
+            else
+                classifier_best<G::DIM>(wcls, xs, a.vocab, best_v, best_i);
             __syncthreads();
             // Layer 0's QKV rows stream into LDS during the argmax exchange.
             stage_qkv(0);

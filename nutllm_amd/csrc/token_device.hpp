@@ -648,6 +648,174 @@ __device__ __forceinline__ void classifier_best(const float *cls, const float *x
     }
 }
 
+// The fp32 logit of classifier row `row` against x (xs, DIM floats in plain
+// order), in every lane: the arithmetic of classifier_best, so both give
+// the same value for a row.
+template <int DIM, bool FRESH = false>
+__device__ __forceinline__ float classifier_row(const float *cls, const float *xs, int row)
+{
+    const int lane = FRESH ? opaque_lane_value(threadIdx.x & (kWave - 1))
+                           : int(threadIdx.x & (kWave - 1));
+    constexpr int C4 = DIM / 4 / kWave;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    const float4 *w0 = reinterpret_cast<const float4 *>(cls + size_t(row) * DIM);
+    float s0 = 0.0f;
+#pragma unroll
+    for (int j0 = 0; j0 < C4; j0 += 4) {
+        float4 v0[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v0[j] = w0[lane + kWave * (j0 + j)];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 x = x4[lane + kWave * (j0 + j)];
+            s0 = fmaf(v0[j].x, x.x, s0);
+            s0 = fmaf(v0[j].y, x.y, s0);
+            s0 = fmaf(v0[j].z, x.z, s0);
+            s0 = fmaf(v0[j].w, x.w, s0);
+        }
+    }
+    return wave_total(s0);
+}
+
+// Rows of the workgroup's classifier share one screened argmax can track:
+// an upper bound per row in LDS.
+__host__ __device__ constexpr int screened_rows(int vocab)
+{
+    return (vocab + kGrid - 1) / kGrid;
+}
+
+// This workgroup's share of the classifier (wg_share of the vocab, split
+// over the waves as classifier_best) screened through its fp16 copy: the
+// wave's best (value, row) of the fp32 logits, first row on ties, equal to
+// classifier_best's. cls16 holds row j times 2^e_j in fp16 and screen[j] =
+// (c_j, 2^-e_j) with |s_j - a_j| <= ||x||_2 c_j, s_j the fp32 logit
+// (classifier_row), a_j the copy's logit. With E_j that bound (widened by
+// the fp32 rounding of a_j +- E_j), L = max_j (a_j - E_j) over the
+// workgroup's rows and k the row attaining it, every row with a_j + E_j < L
+// has s_j <= a_j + E_j < L <= s_k, so only the other rows (the candidates,
+// k among them) need their fp32 logits: the workgroup reads the fp16 copy,
+// half the fp32 bytes, and a few fp32 rows. A NaN or infinity anywhere
+// makes the rows concerned candidates. upper: LDS, screened_rows(vocab)
+// floats; red: LDS, 2 kWaves floats. Ends without a barrier: red is read
+// until every wave has passed the candidate step.
+template <int DIM, bool FRESH = false>
+__device__ void classifier_screened(const float *cls, const uint16_t *cls16,
+                                    const float2 *screen, const float *xs, int vocab,
+                                    float *upper, float *red, float &best_v, int &best_i)
+{
+    const int lane = FRESH ? opaque_lane_value(threadIdx.x & (kWave - 1))
+                           : int(threadIdx.x & (kWave - 1));
+    const int wave = wave_index();
+    constexpr int C8 = DIM / 8 / kWave; // 8-weight groups per lane per row
+    static_assert(DIM % (8 * kWave) == 0, "whole 8-weight groups per lane");
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    int wb, we, rb, re;
+    wg_share(vocab, wb, we);
+    rb = wb + (we - wb) * wave / kWaves;
+    re = wb + (we - wb) * (wave + 1) / kWaves;
+
+    // ||x||_2 (double sums: no overflow or underflow for any fp32 x)
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < DIM; i += kThreads)
+        ss = fma(double(xs[i]), double(xs[i]), ss);
+    for (int off = kWave / 2; off > 0; off >>= 1)
+        ss += __shfl_xor(ss, off);
+    uint32_t *red_u = reinterpret_cast<uint32_t *>(red); // a double as two words
+    if (lane == 0) {
+        const unsigned long long b = __double_as_longlong(ss);
+        red_u[2 * wave] = uint32_t(b);
+        red_u[2 * wave + 1] = uint32_t(b >> 32);
+    }
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++)
+        total += __longlong_as_double(
+            (long long)((unsigned long long)red_u[2 * w + 1] << 32 | red_u[2 * w]));
+    const float xnorm = float(sqrt(total));
+    __syncthreads();
+
+    // a_j of the fp16 copy, ROWS rows at a time; E_j, the lower bounds' max
+    constexpr int ROWS = 2;
+    float lmax = -INFINITY;
+    for (int row = rb; row < re; row += ROWS) {
+        uint4 w[ROWS][C8];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            const uint4 *p =
+                reinterpret_cast<const uint4 *>(cls16 + size_t(min(row + r, re - 1)) * DIM);
+#pragma unroll
+            for (int k = 0; k < C8; k++)
+                w[r][k] = p[lane + kWave * k];
+        }
+        float acc[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++)
+            acc[r] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < C8; k++) {
+            const int c = lane + kWave * k; // weights 8c .. 8c + 7
+            const float4 xa = x4[2 * c], xb = x4[2 * c + 1];
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) {
+                const uint4 q = w[r][k];
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.x)), xa.x, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.x >> 16)), xa.y, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.y)), xa.z, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.y >> 16)), xa.w, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.z)), xb.x, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.z >> 16)), xb.y, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.w)), xb.z, acc[r]);
+                acc[r] = fmaf(half_bits_to_float(uint16_t(q.w >> 16)), xb.w, acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            if (row + r < re) {
+                const float2 sc = screen[row + r];
+                const float a = wave_total(acc[r]) * sc.y;
+                // the bound, widened by the rounding of a +- e and floored
+                // below the smallest normal scale a logit can carry
+                const float e = fmaf(fabsf(a), 0x1p-22f, xnorm * sc.x) + 0x1p-120f;
+                lmax = fmaxf(lmax, a - e);
+                if (lane == 0)
+                    upper[row + r - wb] = a + e;
+            }
+        }
+    }
+    if (lane == 0)
+        red[wave] = lmax;
+    __syncthreads();
+    float bound = red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; w++)
+        bound = fmaxf(bound, red[w]);
+
+    // candidates in row order, the c-th to wave c % kWaves; exact logits
+    best_v = -INFINITY;
+    best_i = 0x7fffffff;
+    int seen = 0;
+    for (int base = 0; base < we - wb; base += kWave) {
+        const int i = base + lane;
+        const bool cand = i < we - wb && !(upper[i] < bound);
+        unsigned long long mask = __ballot(cand);
+        while (mask != 0) {
+            const int bit = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            if (seen % kWaves == wave) {
+                const int row = wb + base + bit;
+                const float v = classifier_row<DIM, FRESH>(cls, xs, row);
+                if (v > best_v || (v == best_v && row < best_i)) {
+                    best_v = v;
+                    best_i = row;
+                }
+            }
+            seen++;
+        }
+    }
+}
+
 // First-index argmax over the grid from every wave's best (value, row):
 // the workgroup's best is published as two tagged words in x_part
 // (value, then index at x_part + kGrid), and every workgroup reduces all

@@ -117,14 +117,18 @@ class SynthModel:
             m.set_layer(i, mats, *self.layer_norms(i))
         return m
 
-    def weight_bytes_per_token(self):
-        """Algorithmic bytes one decode token streams: packed weights + fp16
-        scales of every projection, fp32 classifier, the 2L+1 norm vectors
-        and one embedding row."""
+    def weight_bytes_per_token(self, screened=False):
+        """Bytes of weights one decode token streams: packed weights + fp16
+        scales of every projection, the classifier, the 2L+1 norm vectors
+        and one embedding row. The classifier is the fp32 matrix, or with
+        `screened` what the token kernels' screened argmax reads instead:
+        its fp16 copy and one (bound, scale) pair per row (the few fp32 rows
+        it recomputes are not counted)."""
         c = self.config
         linear = sum(d.nbytes + s.nbytes for mats in self.layers
                      for (d, s, *_rest) in mats.values())
-        return (linear + c.vocab_size * c.dim * 4 +
+        classifier = c.vocab_size * (c.dim * 2 + 8) if screened else c.vocab_size * c.dim * 4
+        return (linear + classifier +
                 (2 * c.layers + 1) * c.dim * 4 + c.dim * 4)
 
 
