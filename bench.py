@@ -10,12 +10,12 @@ resident in HBM before the timed region.
 value     decode tok/s with the reference's GenerationStats semantics
           (every classifier + argmax + decode step after the prefill).
 roofline  algorithmic bytes of the decode loop (packed weights + fp16 scales
-          + the classifier's fp16 screening copy and row bounds + norms + one
+          + the classifier's INT8 block-32 screening copy + norms + one
           embedding row per token, plus K/V reads) / device time of the
           decode loop from HIP events on the model's stream, against the
           8 TB/s HBM peak. The argmax reads the fp32 classifier rows only
-          for the few rows the fp16 copy's error bounds cannot rule out
-          (not counted).
+          for the few rows the copy's error bounds cannot rule out (not
+          counted).
 model_weight_roofline  the same with the model's own weight bytes (the
           fp32 classifier as stored): weight bytes per token / step time.
           roofline.traffic: HBM bytes per generate launch measured in the same

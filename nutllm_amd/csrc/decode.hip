@@ -374,61 +374,40 @@ __global__ __launch_bounds__(kThreads) void pick_token_kernel(
     }
 }
 
-// The screening copy of the fp32 classifier, one wave per row j: the row
-// times 2^e_j in fp16 (round to nearest; e_j puts the row's largest
-// magnitude in [2^14, 2^15), at most 2^100) and screen[j] = (c_j, 2^-e_j),
-// where c_j bounds |s_j - a_j| / ||x||_2 for any fp32 input x: s_j is the
-// fp32 logit (any summation order of fp32 FMAs), a_j the same sum over the
-// fp16 copy times 2^-e_j. With n = dim, u16 = 2^-11 and gamma = n 2^-24 /
-// (1 - n 2^-24): the copy's error is at most u16 |w| + 2^-14-e_j per weight
-// (2^-14: a flushed subnormal), each sum's rounding at most gamma times its
-// sum of absolute terms, so
-//   c_j = 1.01 (||w_j|| (u16 + gamma (2 + u16)) + 2^-14-e_j sqrt(n) (1 + gamma)),
-// the 1 % covering the fp32 rounding of the norm of x and of the bound
-// itself. A row with a non-finite weight gets c_j = infinity.
+// The screening copy of the fp32 classifier as INT8 block-32 codes, one
+// thread per (row, block): the scale s = the smallest fp16 >= max|w| / 127
+// (so no code needs clamping and |w - s q| <= s / 2), q = rint(w / s) in
+// double. A block with a non-finite weight gets a NaN scale (its rows
+// always stay candidates), an all-zero block s = 0.
 __global__ __launch_bounds__(kThreads) void classifier_screen_kernel(
-    const float *w, int vocab, int dim, uint16_t *w16, float2 *screen)
+    const float *w, int vocab, int dim, int8_t *codes, uint16_t *scales)
 {
-    const int row = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
-    if (row >= vocab)
+    const int blocks = dim / 32;
+    const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= (long long)vocab * blocks)
         return;
-    const float *r = w + size_t(row) * dim;
-    double ss = 0.0;
-    float mx = 0.0f;
+    const float *src = w + i * 32;
+    double m = 0.0;
     bool finite = true;
-    for (int i = lane; i < dim; i += kWave) {
-        const float v = r[i];
-        finite = finite && isfinite(v);
-        mx = fmaxf(mx, fabsf(v));
-        ss = fma(double(v), double(v), ss);
+    for (int k = 0; k < 32; k++) {
+        finite = finite && isfinite(src[k]);
+        m = fmax(m, fabs(double(src[k])));
     }
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        ss += __shfl_xor(ss, off);
-        mx = fmaxf(mx, __shfl_xor(mx, off));
+    uint16_t bits = 0;
+    double s = 0.0;
+    if (!finite) {
+        bits = 0x7e00; // NaN
+    } else if (m > 0.0) {
+        const double t = m / 127.0;
+        bits = __builtin_bit_cast(uint16_t, _Float16(float(t)));
+        if (double(__builtin_bit_cast(_Float16, bits)) < t)
+            bits++; // the next fp16 up (t > 0)
+        s = double(__builtin_bit_cast(_Float16, bits));
     }
-    finite = __all(finite);
-    int e = 0;
-    if (finite && mx > 0.0f) {
-        int k;
-        (void)frexpf(mx, &k); // mx = m 2^k, m in [0.5, 1)
-        e = min(15 - k, 100);
-    }
-    uint16_t *d = w16 + size_t(row) * dim;
-    for (int i = lane; i < dim; i += kWave)
-        d[i] = __builtin_bit_cast(uint16_t, _Float16(finite ? ldexpf(r[i], e) : 0.0f));
-    if (lane == 0) {
-        float c = INFINITY;
-        if (finite) {
-            const double n = dim, u16 = 0x1p-11;
-            const double gamma = n * 0x1p-24 / (1.0 - n * 0x1p-24);
-            const double bound =
-                1.01 * (sqrt(ss) * (u16 + gamma * (2.0 + u16)) +
-                        ldexp(1.0, -14 - e) * sqrt(n) * (1.0 + gamma));
-            c = float(bound * (1.0 + 0x1p-20)); // not below the double value
-        }
-        screen[row] = make_float2(c, ldexpf(1.0f, -e));
-    }
+    int8_t *dst = codes + i * 32;
+    for (int k = 0; k < 32; k++)
+        dst[k] = (finite && s > 0.0) ? int8_t(fmin(127.0, fmax(-127.0, rint(src[k] / s)))) : 0;
+    scales[i] = bits;
 }
 
 __global__ void set_int_kernel(int *target, int value) { *target = value; }
@@ -535,11 +514,12 @@ void launch_classifier(const DecodeShape &s, const float *hidden,
     check_launch("generation: classifier");
 }
 
-void launch_classifier_screen(const float *weights, int vocab, int dim, uint16_t *w16,
-                              float2 *screen, hipStream_t stream)
+void launch_classifier_screen(const float *weights, int vocab, int dim, int8_t *codes,
+                              uint16_t *scales, hipStream_t stream)
 {
-    hipLaunchKernelGGL(classifier_screen_kernel, dim3((vocab + kWaves - 1) / kWaves),
-                       dim3(kThreads), 0, stream, weights, vocab, dim, w16, screen);
+    const long long cells = (long long)vocab * (dim / 32);
+    hipLaunchKernelGGL(classifier_screen_kernel, dim3(unsigned((cells + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, stream, weights, vocab, dim, codes, scales);
     check_launch("classifier screening copy");
 }
 

@@ -93,11 +93,11 @@ void launch_classifier(const DecodeShape &s, const float *hidden,
                        const float *final_norm, const float *weights,
                        float *logits, float *part_val, int *part_idx,
                        const StepState *state, hipStream_t stream);
-// The classifier's screening copy for the token kernels' argmax: each row
-// in fp16 times 2^e_j (w16, vocab x dim) and screen[j] = (c_j, 2^-e_j) with
-// |fp32 logit - screened logit| <= ||x||_2 c_j for every input x.
-void launch_classifier_screen(const float *weights, int vocab, int dim, uint16_t *w16,
-                              float2 *screen, hipStream_t stream);
+// The classifier's screening copy for the token kernels' argmax: INT8
+// block-32 codes (vocab x dim) and fp16 block scales (vocab x dim / 32),
+// each scale the smallest fp16 >= the block's max |w| / 127.
+void launch_classifier_screen(const float *weights, int vocab, int dim, int8_t *codes,
+                              uint16_t *scales, hipStream_t stream);
 // Reduce the partials to the first maximal index; on eos set done, else
 // append to tokens and make it the next input token.
 void launch_pick_token(const DecodeShape &s, const float *part_val,

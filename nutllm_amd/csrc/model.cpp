@@ -511,28 +511,27 @@ bool use_token_kernel(nut_model &m, size_t end_length)
     return ok;
 }
 
-// The classifier's screening copy (launch_classifier_screen) for the
+// The classifier's INT8 screening copy (launch_classifier_screen) for the
 // generate loop, when the vocabulary's share per workgroup fits the
 // kernel's bound array; null otherwise.
-void prepare_screen(nut_model &m, const uint16_t *&w16, const float2 *&screen)
+void prepare_screen(nut_model &m, const uint8_t *&codes, const uint16_t *&scales)
 {
-    w16 = nullptr;
-    screen = nullptr;
+    codes = nullptr;
+    scales = nullptr;
     const int vocab = m.shape.vocab, dim = m.shape.dim;
-    if ((vocab + kTokenGrid - 1) / kTokenGrid > kScreenRowsMax)
+    if ((vocab + kTokenGrid - 1) / kTokenGrid > kScreenRowsMax || dim % 32 != 0)
         return;
     if (!m.screen_ready) {
-        if (m.classifier16.get() == nullptr) {
-            m.classifier16.allocate(size_t(vocab) * dim * sizeof(uint16_t));
-            m.classifier_screen.allocate(size_t(vocab) * sizeof(float2));
+        if (m.classifier8.get() == nullptr) {
+            m.classifier8.allocate(size_t(vocab) * dim);
+            m.classifier8_scales.allocate(size_t(vocab) * (dim / 32) * sizeof(uint16_t));
         }
-        launch_classifier_screen(m.output_weights(), vocab, dim,
-                                 m.classifier16.as<uint16_t>(),
-                                 m.classifier_screen.as<float2>(), m.stream);
+        launch_classifier_screen(m.output_weights(), vocab, dim, m.classifier8.as<int8_t>(),
+                                 m.classifier8_scales.as<uint16_t>(), m.stream);
         m.screen_ready = true;
     }
-    w16 = m.classifier16.as<uint16_t>();
-    screen = m.classifier_screen.as<float2>();
+    codes = m.classifier8.as<uint8_t>();
+    scales = m.classifier8_scales.as<uint16_t>();
 }
 
 void prepare_token_kernel(nut_model &m)
@@ -560,7 +559,7 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.final_norm = m.final_norm.as<float>();
     a.classifier = m.output_weights();
     if (classify)
-        prepare_screen(m, a.classifier16, a.classifier_screen);
+        prepare_screen(m, a.classifier8, a.classifier8_scales);
     a.rope = m.rope.as<float2>();
     a.k_cache = kv.keys.as<float>();
     a.v_cache = kv.values.as<float>();

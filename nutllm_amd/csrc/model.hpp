@@ -56,9 +56,9 @@ struct nut_model {
     nut::DecodeShape shape{};
     std::vector<nut::DeviceLayer> layers;
     nut::DeviceBuffer embeddings, final_norm, lm_head, rope;
-    // The classifier's fp16 screening copy and per-row bounds for the token
-    // kernels' argmax, built at the first generate after set_globals.
-    nut::DeviceBuffer classifier16, classifier_screen;
+    // The classifier's INT8 screening copy (codes, block scales) for the
+    // token kernels' argmax, built at the first generate after set_globals.
+    nut::DeviceBuffer classifier8, classifier8_scales;
     bool screen_ready = false;
     // Weight arena: layer l at arena + l * layout.bytes (LayerLayout).
     nut::DeviceBuffer arena;

@@ -252,6 +252,8 @@ template <class G> struct Lds {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
     static_assert(kWaves * G::HPW * G::NP >= kScreenRowsMax,
                   "the screened classifier's upper bounds fit the scores region");
+    static_assert(G::R1 >= 4 * G::DIM && G::DIM + 2 * G::KVD >= G::DIM / 32,
+                  "the classifier's x in region 1, its block sums of |x| over q/k/v");
 };
 
 // CLASSIFY: the generate loop (classifier + argmax first in every
@@ -373,21 +375,27 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
             }
             const float scale = rms_scale(wg_sum(sq, red), G::DIM);
-            // plain layout: lane needs x[4c..4c+3], c = lane + 64 j
+            // x in plain layout (lane needs x[4c..4c+3], c = lane + 64 j) in
+            // region 1, free until layer 0's rows are staged; its digits
+            // for the screened argmax in xl / xsc, its block sums of |x|
+            // over the q/k/v staging, the row bounds over the scores
+            float *xcls = reinterpret_cast<float *>(r1);
 #pragma unroll
             for (int u = 0; u < Slice<G::DIM>::PER; u++) {
                 const int i = threadIdx.x + u * kThreads;
                 if (i < G::DIM)
-                    xs[i] = h_raw[i] * scale * nw.v[u];
+                    xcls[i] = h_raw[i] * scale * nw.v[u];
             }
             __syncthreads();
             float best_v;
             int best_i;
-            if (a.classifier16 != nullptr)
-                classifier_screened<G::DIM>(wcls, a.classifier16, a.classifier_screen, xs,
-                                            a.vocab, scores, red, best_v, best_i);
-            else
-                classifier_best<G::DIM>(wcls, xs, a.vocab, best_v, best_i);
+            if (a.classifier8 != nullptr) {
+                screen_x_digits<G::DIM>(xcls, xl, xsc, qkv);
+                classifier_screened<G::DIM>(wcls, a.classifier8, a.classifier8_scales, xcls, xl,
+                                            xsc, qkv, a.vocab, scores, red, best_v, best_i);
+            } else {
+                classifier_best<G::DIM>(wcls, xcls, a.vocab, best_v, best_i);
+            }
             __syncthreads();
             // Layer 0's QKV rows stream into LDS during the argmax exchange.
             stage_qkv(0);

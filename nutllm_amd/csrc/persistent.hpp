@@ -20,10 +20,10 @@ struct TokenArgs {
     // Weight arena: layer l at weights + l * layer_layout(...).bytes.
     const uint8_t *weights;
     const float *embeddings, *final_norm, *classifier;
-    // The classifier's screening copy (launch_classifier_screen), or null
-    // for the plain fp32 pass over every row.
-    const uint16_t *classifier16;
-    const float2 *classifier_screen;
+    // The classifier's INT8 screening copy (launch_classifier_screen): codes
+    // and block scales, or null for the plain fp32 pass over every row.
+    const uint8_t *classifier8;
+    const uint16_t *classifier8_scales;
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
     uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
@@ -53,8 +53,8 @@ struct TokenArgs {
 };
 
 // Largest share of classifier rows per workgroup for which the generate
-// loop screens the classifier through its fp16 copy (TokenArgs::
-// classifier16); larger vocabularies take the plain fp32 pass.
+// loop screens the classifier through its INT8 copy (TokenArgs::
+// classifier8); larger vocabularies take the plain fp32 pass.
 constexpr int kScreenRowsMax = 1024;
 
 // Exchange tags. Every exchange word is (tag << 32) | value, and a launch

@@ -685,99 +685,117 @@ __host__ __device__ constexpr int screened_rows(int vocab)
     return (vocab + kGrid - 1) / kGrid;
 }
 
+// The screened argmax's input: INT8 digits of x (quartet_digits<0>) in xl
+// and xsc, and xl1[b] = sum of |x_k| over block b, for a DIM-vector x in
+// LDS. Ends with a barrier.
+template <int DIM>
+__device__ void screen_x_digits(const float *x, uint32_t *xl, float *xsc, float *xl1)
+{
+    static_assert(DIM % (4 * kThreads) == 0, "whole quartets per thread");
+#pragma unroll
+    for (int u = 0; u < DIM / (4 * kThreads); u++) {
+        const int t = threadIdx.x + kThreads * u; // quartet t of x
+        const float4 v = reinterpret_cast<const float4 *>(x)[t];
+        float l1 = (fabsf(v.x) + fabsf(v.y)) + (fabsf(v.z) + fabsf(v.w));
+        l1 += dpp<kDppQuadSwap1>(l1, 0.0f);
+        l1 += dpp<kDppQuadSwap2>(l1, 0.0f);
+        l1 += dpp<kDppRowHalfMirror>(l1, 0.0f);
+        if ((t & 7) == 0)
+            xl1[t >> 3] = l1;
+        quartet_digits<0>(v, t >> 3, t & 7, xl, xsc);
+    }
+    __syncthreads();
+}
+
+// Bound factor of the screened argmax for rows of n weights:
+// |s_j - a_j| <= kappa(n) T_j with T_j = sum_b s_jb ||x_b||_1 (s_jb the
+// block scales of the INT8 copy, x_b the input's blocks). Terms: the copy's
+// rounding, |w - s q| <= s / 2 (the scale rounded up, so no code clamps;
+// 2^-10 more for the fp32 quotient); the fp32 rounding of the exact logit,
+// gamma_n sum |w_k x_k| <= gamma_n 127 T_j (|w_k| <= 127 s_jb); the digits
+// of x, |x_k - xsc X_k| <= 3 xsc_b with xsc_b <= ||x_b||_1 / 7e6, and the
+// fp32 sum over blocks (0.0025 covers both); 1 % over all for the fp32
+// rounding of T_j and of the block sums of |x|.
+__host__ __device__ constexpr float screen_kappa(int n)
+{
+    return float(1.01 * (0.5 * (1.0 + 1.0 / 1024) + 127.0 * (n * 0x1p-24 / (1.0 - n * 0x1p-24)) +
+                         0.0025));
+}
+
 // This workgroup's share of the classifier (wg_share of the vocab, split
-// over the waves as classifier_best) screened through its fp16 copy: the
-// wave's best (value, row) of the fp32 logits, first row on ties, equal to
-// classifier_best's. cls16 holds row j times 2^e_j in fp16 and screen[j] =
-// (c_j, 2^-e_j) with |s_j - a_j| <= ||x||_2 c_j, s_j the fp32 logit
-// (classifier_row), a_j the copy's logit. With E_j that bound (widened by
-// the fp32 rounding of a_j +- E_j), L = max_j (a_j - E_j) over the
-// workgroup's rows and k the row attaining it, every row with a_j + E_j < L
-// has s_j <= a_j + E_j < L <= s_k, so only the other rows (the candidates,
-// k among them) need their fp32 logits: the workgroup reads the fp16 copy,
-// half the fp32 bytes, and a few fp32 rows. A NaN or infinity anywhere
-// makes the rows concerned candidates. upper: LDS, screened_rows(vocab)
-// floats; red: LDS, 2 kWaves floats. Ends without a barrier: red is read
-// until every wave has passed the candidate step.
+// over the waves as classifier_best) screened through an INT8 block-32 copy:
+// the wave's best (value, row) of the fp32 logits, first row on ties, equal
+// to classifier_best's. The copy holds row j as codes q (c8, DIM bytes per
+// row) and fp16 block scales s_jb rounded up from max|w| / 127 (c8s). Its
+// logit a_j = sum_b s_jb xsc_b (integer block dot of q and the digits of
+// x) satisfies |s_j - a_j| <= E_j = screen_kappa(DIM) T_j, s_j the fp32
+// logit (classifier_row), widened by the fp32 rounding of a_j +- E_j. With
+// L = max_j (a_j - E_j) over the workgroup's rows and k the row attaining
+// it, every row with a_j + E_j < L has s_j <= a_j + E_j < L <= s_k, so only
+// the other rows (the candidates, k among them) need their fp32 logits:
+// the workgroup reads 2,176 bytes per row instead of 8,192, and a few fp32
+// rows. A NaN or infinity anywhere makes the rows concerned candidates.
+// xs: x (DIM floats, plain order); xl, xsc, xl1: screen_x_digits of x;
+// upper: LDS, screened_rows(vocab) floats; red: LDS, kWaves floats. Ends
+// without a barrier: red is read until every wave has passed the candidate
+// step.
 template <int DIM, bool FRESH = false>
-__device__ void classifier_screened(const float *cls, const uint16_t *cls16,
-                                    const float2 *screen, const float *xs, int vocab,
-                                    float *upper, float *red, float &best_v, int &best_i)
+__device__ void classifier_screened(const float *cls, const uint8_t *c8, const uint16_t *c8s,
+                                    const float *xs, const uint32_t *xl, const float *xsc,
+                                    const float *xl1, int vocab, float *upper, float *red,
+                                    float &best_v, int &best_i)
 {
     const int lane = FRESH ? opaque_lane_value(threadIdx.x & (kWave - 1))
                            : int(threadIdx.x & (kWave - 1));
     const int wave = wave_index();
-    constexpr int C8 = DIM / 8 / kWave; // 8-weight groups per lane per row
-    static_assert(DIM % (8 * kWave) == 0, "whole 8-weight groups per lane");
-    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    constexpr int BLK = DIM / 32, CPL = BLK / kWave; // blocks per lane
+    static_assert(BLK % kWave == 0, "whole blocks per lane");
     int wb, we, rb, re;
     wg_share(vocab, wb, we);
     rb = wb + (we - wb) * wave / kWaves;
     re = wb + (we - wb) * (wave + 1) / kWaves;
-
-    // ||x||_2 (double sums: no overflow or underflow for any fp32 x)
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < DIM; i += kThreads)
-        ss = fma(double(xs[i]), double(xs[i]), ss);
-    for (int off = kWave / 2; off > 0; off >>= 1)
-        ss += __shfl_xor(ss, off);
-    uint32_t *red_u = reinterpret_cast<uint32_t *>(red); // a double as two words
-    if (lane == 0) {
-        const unsigned long long b = __double_as_longlong(ss);
-        red_u[2 * wave] = uint32_t(b);
-        red_u[2 * wave + 1] = uint32_t(b >> 32);
-    }
-    __syncthreads();
-    double total = 0.0;
+    XDigits<CPL> x;
+    load_x(x, xl, xsc, BLK);
+    float l1[CPL];
 #pragma unroll
-    for (int w = 0; w < kWaves; w++)
-        total += __longlong_as_double(
-            (long long)((unsigned long long)red_u[2 * w + 1] << 32 | red_u[2 * w]));
-    const float xnorm = float(sqrt(total));
-    __syncthreads();
+    for (int j = 0; j < CPL; j++)
+        l1[j] = xl1[lane + kWave * j];
+    constexpr float kappa = screen_kappa(DIM);
 
-    // a_j of the fp16 copy, ROWS rows at a time; E_j, the lower bounds' max
-    constexpr int ROWS = 2;
+    // a_j and T_j of the INT8 copy, ROWS rows at a time; E_j, the lower
+    // bounds' max
+    constexpr int ROWS = 4;
     float lmax = -INFINITY;
     for (int row = rb; row < re; row += ROWS) {
-        uint4 w[ROWS][C8];
+        uint4 w[ROWS][CPL][2];
+        uint16_t sc[ROWS][CPL];
 #pragma unroll
         for (int r = 0; r < ROWS; r++) {
-            const uint4 *p =
-                reinterpret_cast<const uint4 *>(cls16 + size_t(min(row + r, re - 1)) * DIM);
+            const int rr = min(row + r, re - 1);
+            const uint4 *p = reinterpret_cast<const uint4 *>(c8 + size_t(rr) * DIM);
 #pragma unroll
-            for (int k = 0; k < C8; k++)
-                w[r][k] = p[lane + kWave * k];
-        }
-        float acc[ROWS];
-#pragma unroll
-        for (int r = 0; r < ROWS; r++)
-            acc[r] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < C8; k++) {
-            const int c = lane + kWave * k; // weights 8c .. 8c + 7
-            const float4 xa = x4[2 * c], xb = x4[2 * c + 1];
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) {
-                const uint4 q = w[r][k];
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.x)), xa.x, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.x >> 16)), xa.y, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.y)), xa.z, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.y >> 16)), xa.w, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.z)), xb.x, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.z >> 16)), xb.y, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.w)), xb.z, acc[r]);
-                acc[r] = fmaf(half_bits_to_float(uint16_t(q.w >> 16)), xb.w, acc[r]);
+            for (int j = 0; j < CPL; j++) {
+                const int b = lane + kWave * j;
+                w[r][j][0] = p[2 * b];
+                w[r][j][1] = p[2 * b + 1];
+                sc[r][j] = c8s[size_t(rr) * BLK + b];
             }
         }
 #pragma unroll
         for (int r = 0; r < ROWS; r++) {
+            float ap = 0.0f, tp = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; j++) {
+                const float s = half_bits_to_float(sc[r][j]);
+                ap = fmaf(s * x.sc[j], dot_words_digits<0>(w[r][j], x.d[j]), ap);
+                tp = fmaf(s, l1[j], tp);
+            }
             if (row + r < re) {
-                const float2 sc = screen[row + r];
-                const float a = wave_total(acc[r]) * sc.y;
+                const float a = wave_total(ap);
+                const float t = wave_total(tp);
                 // the bound, widened by the rounding of a +- e and floored
                 // below the smallest normal scale a logit can carry
-                const float e = fmaf(fabsf(a), 0x1p-22f, xnorm * sc.x) + 0x1p-120f;
+                const float e = fmaf(fabsf(a), 0x1p-22f, kappa * t) + 0x1p-120f;
                 lmax = fmaxf(lmax, a - e);
                 if (lane == 0)
                     upper[row + r - wb] = a + e;

@@ -84,7 +84,7 @@ struct Wide {
 // ST_GU until phase C has used them; phase D holds the activation as floats
 // over XD, H and the start of ST_GU (ACT); phase A's q/k/v rows are staged
 // at ST_A, clear of XD and H. The classifier's normalised x sits at ST_GU,
-// the screened classifier's per-row upper bounds after it.
+// its block sums of |x| and the screened argmax's row bounds after it.
 template <class G> struct WideLds {
     static constexpr int XD = 0;
     static constexpr int H = XD + kLimbStride * G::BLK_DIM * 4;
@@ -104,8 +104,8 @@ template <class G> struct WideLds {
                   "16-byte aligned regions");
     static_assert(ST_A >= H + G::DIM * 4, "q/k staging clear of the digits and h");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
-    static_assert(G::ST_GU_BYTES >= (G::DIM + kScreenRowsMax) * 4,
-                  "the classifier's x and the screened classifier's bounds at ST_GU");
+    static_assert(G::ST_GU_BYTES >= (G::DIM + G::BLK_DIM + kScreenRowsMax) * 4,
+                  "the classifier's x, its block sums and the row bounds at ST_GU");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -489,13 +489,18 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             __syncthreads();
             float best_v;
             int best_i;
-            if (a.classifier16 != nullptr)
-                classifier_screened<G::DIM, true>(fresh(a.classifier), fresh(a.classifier16),
-                                                  fresh(a.classifier_screen), xcls, a.vocab,
-                                                  xcls + G::DIM, red, best_v, best_i);
-            else
+            if (a.classifier8 != nullptr) {
+                // digits in XD / XSC, block sums of |x| and row bounds at
+                // ST_GU after x
+                float *xl1 = xcls + G::DIM, *upper = xl1 + G::BLK_DIM;
+                screen_x_digits<G::DIM>(xcls, xl, xsc, xl1);
+                classifier_screened<G::DIM, true>(fresh(a.classifier), fresh(a.classifier8),
+                                                  fresh(a.classifier8_scales), xcls, xl, xsc,
+                                                  xl1, a.vocab, upper, red, best_v, best_i);
+            } else {
                 classifier_best<G::DIM, true>(fresh(a.classifier), xcls, a.vocab, best_v,
                                               best_i);
+            }
             // every wave is past its reads of x before the q/k rows land
             __syncthreads();
             // layer 0's inputs stream during the argmax exchange

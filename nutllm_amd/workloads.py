@@ -122,12 +122,13 @@ class SynthModel:
         scales of every projection, the classifier, the 2L+1 norm vectors
         and one embedding row. The classifier is the fp32 matrix, or with
         `screened` what the token kernels' screened argmax reads instead:
-        its fp16 copy and one (bound, scale) pair per row (the few fp32 rows
-        it recomputes are not counted)."""
+        its INT8 block-32 copy, codes and fp16 scales (the few fp32 rows it
+        recomputes are not counted)."""
         c = self.config
         linear = sum(d.nbytes + s.nbytes for mats in self.layers
                      for (d, s, *_rest) in mats.values())
-        classifier = c.vocab_size * (c.dim * 2 + 8) if screened else c.vocab_size * c.dim * 4
+        classifier = (c.vocab_size * (c.dim + c.dim // 16) if screened
+                      else c.vocab_size * c.dim * 4)
         return (linear + classifier +
                 (2 * c.layers + 1) * c.dim * 4 + c.dim * 4)
 

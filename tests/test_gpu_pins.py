@@ -9,11 +9,11 @@
   reference's std::max_element): identical classifier rows in the same
   wave's row pair, across waves and across workgroups, through the token
   kernel and the step path's classifier + pick.
-* The token kernel's screened classifier (an fp16 copy with per-row error
-  bounds, fp32 logits only for the rows the bounds cannot rule out) returns
-  the fp32 argmax when two rows' fp16 copies are identical but their fp32
-  logits differ by far more than fp32 rounding: the larger one wins in
-  either index order.
+* The token kernel's screened classifier (an INT8 block-32 copy with
+  error bounds, fp32 logits only for the rows the bounds cannot rule out)
+  returns the fp32 argmax when two rows' INT8 copies are identical but
+  their fp32 logits differ by far more than fp32 rounding: the larger one
+  wins in either index order.
 * QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156) equal
   to the value the reference computed for the same model.
 * The token kernel's exchange tags across a restart of their 32-bit range.
@@ -185,33 +185,33 @@ def test_argmax_first_index_on_device_ties(gpu, tie_model, path, offset):
         dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
 
 
+def screen_scales(row):
+    """Block-32 scales of the screening copy: the smallest fp16 at or above
+    each block's max |w| / 127."""
+    t = np.max(np.abs(row.reshape(-1, 32).astype(np.float64)), axis=1) / 127.0
+    h = t.astype(np.float16)
+    low = h.astype(np.float64) < t
+    h[low] = np.nextafter(h[low], np.float16(np.inf))
+    return h.astype(np.float64)
+
+
 def screen_twin(row, x, up):
-    """A copy of classifier row `row` whose fp16 screening copy (the row
-    times 2^e in fp16, e putting the largest magnitude in [2^14, 2^15)) is
-    bit-identical to the row's, with the 64 weights of largest |x| moved to
-    the far end of their fp16 rounding interval: towards larger logits
-    (up) or smaller ones."""
+    """A copy of classifier row `row` whose INT8 screening copy (block-32
+    codes rint(w / s), s = screen_scales) is identical to the row's: every
+    weight but each block's largest moves half way to the edge of its code's
+    rounding interval, towards larger logits (up) or smaller ones."""
     row = np.asarray(row, np.float32)
-    _, k = np.frexp(np.max(np.abs(row)))
-    e = min(15 - int(k), 100)
-    scaled = np.ldexp(row.astype(np.float64), e)
-    h = scaled.astype(np.float16).astype(np.float64)
-    twin = row.copy()
-    keep = np.argmax(np.abs(row))  # the row's scale stays as it was
-    for i in np.argsort(-np.abs(x))[:65]:
-        if i == keep:
-            continue
-        toward = 1.0 if (x[i] > 0) == up else -1.0
-        nxt = float(np.nextafter(np.float16(h[i]), np.float16(toward * np.inf)))
-        mid = (h[i] + nxt) / 2.0  # the fp16 rounding boundary on that side
-        v = np.float32(np.ldexp(mid, -e))
-        while np.float16(np.ldexp(np.float64(v), e)) != np.float16(h[i]):
-            v = np.nextafter(v, np.float32(row[i]))  # strictly inside the interval
-        twin[i] = v
-    twin_h = np.ldexp(twin.astype(np.float64), e).astype(np.float16)
-    assert np.array_equal(twin_h.view(np.uint16), h.astype(np.float16).view(np.uint16))
-    _, k2 = np.frexp(np.max(np.abs(twin)))
-    assert k2 == k
+    s = np.repeat(screen_scales(row), 32)
+    q = np.rint(row / s)
+    big = np.zeros(row.size, bool)
+    big[np.argmax(np.abs(row.reshape(-1, 32)), axis=1) + 32 * np.arange(row.size // 32)] = True
+    toward = np.where((x > 0) == up, 1.0, -1.0)
+    edge = (q + 0.5 * toward) * s
+    twin = np.where(big, row, (row + 0.5 * (edge - row)).astype(np.float32)).astype(np.float32)
+    keep = np.abs(twin) >= np.repeat(np.max(np.abs(row.reshape(-1, 32)), axis=1), 32)
+    twin[keep & ~big] = row[keep & ~big]  # no block maximum changes
+    assert np.array_equal(screen_scales(twin), screen_scales(row))
+    assert np.array_equal(np.rint(twin / s), q)
     return twin
 
 
@@ -220,9 +220,9 @@ def screen_twin(row, x, up):
 @pytest.mark.parametrize("path", [1, 2], ids=["steps", "token"])
 def test_argmax_screen_near_ties(gpu, tie_model, path, offset, up):
     """Row top + offset becomes a twin of the argmax row `top` with the same
-    fp16 screening copy and an fp32 logit larger (up) or smaller by about
-    1e-4, far above fp32 rounding: the first id is the larger logit's row,
-    which a screen that broke fp16 ties by index would miss (the twin has
+    INT8 screening copy and an fp32 logit larger (up) or smaller, far above
+    fp32 rounding: the first id is the larger logit's row, which a screen
+    that broke ties of the copy's logits by index would miss (the twin has
     the higher index when larger, the lower when smaller), and the greedy
     run equals the oracle's on the same weights."""
     model, prompt, top, dev = tie_model
