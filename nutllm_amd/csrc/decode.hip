@@ -386,27 +386,50 @@ __global__ __launch_bounds__(kThreads) void classifier_screen_kernel(
     const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
     if (i >= (long long)vocab * blocks)
         return;
-    const float *src = w + i * 32;
-    double m = 0.0;
+    float v[32];
+    const float4 *src = reinterpret_cast<const float4 *>(w + i * 32);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 f = src[k];
+        v[4 * k] = f.x;
+        v[4 * k + 1] = f.y;
+        v[4 * k + 2] = f.z;
+        v[4 * k + 3] = f.w;
+    }
+    float m = 0.0f;
     bool finite = true;
+#pragma unroll
     for (int k = 0; k < 32; k++) {
-        finite = finite && isfinite(src[k]);
-        m = fmax(m, fabs(double(src[k])));
+        finite = finite && isfinite(v[k]);
+        m = fmaxf(m, fabsf(v[k]));
     }
     uint16_t bits = 0;
-    double s = 0.0;
+    double inv = 0.0;
     if (!finite) {
         bits = 0x7e00; // NaN
-    } else if (m > 0.0) {
-        const double t = m / 127.0;
+    } else if (m > 0.0f) {
+        const double t = double(m) / 127.0;
         bits = __builtin_bit_cast(uint16_t, _Float16(float(t)));
         if (double(__builtin_bit_cast(_Float16, bits)) < t)
             bits++; // the next fp16 up (t > 0)
-        s = double(__builtin_bit_cast(_Float16, bits));
+        // w / s as w * (1 / s) in double: off the exact quotient by far
+        // less than the 2^-10 s the bound allows beyond s / 2
+        inv = 1.0 / double(__builtin_bit_cast(_Float16, bits));
     }
-    int8_t *dst = codes + i * 32;
-    for (int k = 0; k < 32; k++)
-        dst[k] = (finite && s > 0.0) ? int8_t(fmin(127.0, fmax(-127.0, rint(src[k] / s)))) : 0;
+    uint32_t packed[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const double q = fmin(127.0, fmax(-127.0, rint(double(v[4 * k + e]) * inv)));
+            word |= uint32_t(uint8_t(int8_t(q))) << (8 * e);
+        }
+        packed[k] = word;
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(codes + i * 32);
+    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
     scales[i] = bits;
 }
 
