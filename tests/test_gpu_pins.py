@@ -13,7 +13,8 @@
   error bounds, fp32 logits only for the rows the bounds cannot rule out)
   returns the fp32 argmax when two rows' INT8 copies are identical but
   their fp32 logits differ by far more than fp32 rounding: the larger one
-  wins in either index order.
+  wins in either index order; rows with a NaN or infinite weight behave
+  as in the plain fp32 pass.
 * QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156) equal
   to the value the reference computed for the same model.
 * The token kernel's exchange tags across a restart of their 32-bit range.
@@ -245,6 +246,43 @@ def test_argmax_screen_near_ties(gpu, tie_model, path, offset, up):
                             model.layers)
         ref, _, _ = O.oracle_model(twin).generate(prompt, 4)
         assert ids == ref
+    finally:
+        dev.set_path(0)
+        dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
+
+
+@pytest.mark.parametrize("poison", ["nan-top", "inf-other"])
+@pytest.mark.parametrize("path", [1, 2], ids=["steps", "token"])
+def test_argmax_nonfinite_classifier_rows(gpu, tie_model, path, poison):
+    """A NaN weight in the argmax row makes its logit NaN, which never wins
+    the first-max scan (src/generate.cpp:24-30): the next row does. A +inf
+    weight against a positive x element makes another row's logit +inf,
+    which wins. The screened argmax keeps every row with a non-finite block
+    as a candidate, so both paths give the oracle's ids."""
+    model, prompt, top, dev = tie_model
+    om = O.oracle_model(model)
+    hidden = np.asarray(om.prefill(prompt), np.float64)
+    x = hidden / np.sqrt(np.mean(hidden * hidden) + 1e-5) * model.final_norm
+    head = model.lm_head.copy()
+    if poison == "nan-top":
+        assert top != 0  # a NaN at row 0 would be the scan's answer
+        head[top, 7] = np.nan
+    else:
+        other = (top + 321) % model.config.vocab_size
+        head[other, int(np.argmax(x))] = np.inf
+    dev.set_globals(model.embeddings, model.final_norm, head)
+    try:
+        dev.set_path(path)
+        ids, _ = dev.generate(prompt, 4)
+        bad = W.SynthModel(model.config, model.qtype, model.seed,
+                           model.embeddings, model.final_norm, head,
+                           model.layers)
+        ref, _, _ = O.oracle_model(bad).generate(prompt, 4)
+        assert ids == ref, (ids, ref, top)
+        if poison == "nan-top":
+            assert ids[0] != top
+        else:
+            assert ids[0] == other
     finally:
         dev.set_path(0)
         dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
