@@ -110,6 +110,18 @@ template <class G> struct WideLds {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// First-poll delays (10 ns ticks of the real-time clock) of the two
+// attention exchanges that no weight DMA precedes: the partial scores of a
+// head group and the context. Polling right after the own publish floods
+// the memory system with coherent reads of words most producers have not
+// written yet. Measured on the Llama-2-7B shape (128 tokens at KV 512-639):
+// none 1,639 us per token; scores 300 ns + context 600 ns 1,627; 1.2 +
+// 2.4 us 1,596-1,597; 1.8 + 2.4 us 1,605; 2.4 + 2.4 us 1,623; 1.2 + 3.6 us
+// 1,631. The other three exchanges (h into A, h after Wo, act) wait behind
+// their phase's weight DMA already; 600 ns more on them cost 9 us.
+constexpr int kWidePollDelayScores = 120;
+constexpr int kWidePollDelayContext = 240;
+
 // Cache policy of the weight loads: non-temporal (nt, bit 1), as each
 // weight byte is read once per token and the memory-side cache is left to
 // the classifier.
@@ -631,6 +643,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             {
                 uint64_t v[G::PPT][G::GW];
                 const int tid = opaque_lane_value(threadIdx.x);
+                {
+                    const unsigned long long until =
+                        __builtin_amdgcn_s_memrealtime() + kWidePollDelayScores;
+                    while (__builtin_amdgcn_s_memrealtime() < until)
+                        __builtin_amdgcn_s_sleep(1);
+                }
 #pragma unroll
                 for (int u = 0; u < G::PPT; u++) {
                     const int p = tid + kThreads * u;
@@ -719,7 +737,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             mark(it, 5 + 13 * l);
 
             // ------------------------------------ Wo rows + residual --
-            take<G::DIM, false, true>(fresh(a.x_ctx), hbuf, tag - 1, error);
+            take<G::DIM, false, true, kWidePollDelayContext>(fresh(a.x_ctx), hbuf, tag - 1,
+                                                             error);
             {
                 float4 ones[G::XQ];
 #pragma unroll
