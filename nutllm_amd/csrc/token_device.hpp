@@ -738,8 +738,9 @@ __host__ __device__ constexpr float screen_kappa(int n)
 // xs: x (DIM floats, plain order); xl, xsc, xl1: screen_x_digits of x;
 // upper: LDS, screened_rows(vocab) floats; red: LDS, kWaves floats. Ends
 // without a barrier: red is read until every wave has passed the candidate
-// step.
-template <int DIM, bool FRESH = false>
+// step. ROWS: rows whose loads a wave issues together (measured: 1 to 4 the
+// same for dim 2048; 1 is 6 us per token faster than 4 for dim 4096).
+template <int DIM, bool FRESH = false, int ROWS = 4>
 __device__ void classifier_screened(const float *cls, const uint8_t *c8, const uint16_t *c8s,
                                     const float *xs, const uint32_t *xl, const float *xsc,
                                     const float *xl1, int vocab, float *upper, float *red,
@@ -764,7 +765,6 @@ __device__ void classifier_screened(const float *cls, const uint8_t *c8, const u
 
     // a_j and T_j of the INT8 copy, ROWS rows at a time; E_j, the lower
     // bounds' max
-    constexpr int ROWS = 4;
     float lmax = -INFINITY;
     for (int row = rb; row < re; row += ROWS) {
         uint4 w[ROWS][CPL][2];

@@ -506,7 +506,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 // ST_GU after x
                 float *xl1 = xcls + G::DIM, *upper = xl1 + G::BLK_DIM;
                 screen_x_digits<G::DIM>(xcls, xl, xsc, xl1);
-                classifier_screened<G::DIM, true>(fresh(a.classifier), fresh(a.classifier8),
+                classifier_screened<G::DIM, true, 1>(fresh(a.classifier), fresh(a.classifier8),
                                                   fresh(a.classifier8_scales), xcls, xl, xsc,
                                                   xl1, a.vocab, upper, red, best_v, best_i);
             } else {
