@@ -35,14 +35,20 @@ namespace {
 // producers have not written yet, and 256 workgroups doing so flood the
 // memory system with coherent reads that slow every producer's publish and
 // every consumer's later rounds. Measured per exchange (TinyLlama INT4, 16
-// tokens: 423 us per token with no delays, 388 with these; INT8 at KV
-// 2048-2175, split attention: 602 -> 514): into phases A (h after W2) and D
-// (act) 450 ns, into B (q/k/v) and C (h after Wo), which follow a larger
+// tokens: 423 us per token with no delays, 388 with the first set; INT8 at
+// KV 2048-2175, split attention: 602 -> 514): into phases A (h after W2) and
+// D (act) 450 ns, into B (q/k/v) and C (h after Wo), which follow a larger
 // weight DMA that already delays their polls, 150 ns; with split attention
-// 600 and 300 ns, and 900 ns for its partials and merged context.
+// 600 and 300 ns, and 900 ns for its partials and merged context. Re-swept
+// for the fused attention once the attention scores and the classifier
+// had become faster: A 300, B 50, C 150, D 600 ns (361.2 -> 357.7 us per
+// token, two alternating runs each on one box). Other points of the
+// sweep: A 150, B 0 366.9 against 360.2 for the first set; A 450, B 0,
+// D 600 359.0 and A 300, B 0, D 900 361.7 against 358.5 for A 300, B 0,
+// D 600.
 template <bool LONG> struct PollDelay {
-    static constexpr int A = LONG ? 60 : 45, B = LONG ? 30 : 15;
-    static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 45;
+    static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 5;
+    static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 60;
     static constexpr int PARTIALS = 90, CONTEXT = 90;
 };
 
