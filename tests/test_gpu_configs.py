@@ -13,8 +13,11 @@ src/generate.cpp:174-216) over the same seeded weights:
 The device prefills with the batched MFMA path (bar: rel-L2 2e-3 for the
 hidden state and K/V rows) and must reproduce all 128 greedy ids. A
 two-layer model at the 7B widths is also checked against the oracle at the
-fp32 bar (1e-5) on the step kernels and at 2e-3 on the batched prefill.
+fp32 bar (1e-5) on the step kernels and at 2e-3 on the batched prefill,
+and its classifier argmax through the wide kernel's INT8 screen on rows
+built to defeat a screen that ignored the fp32 logits or non-finite rows.
 """
+import dataclasses
 import hashlib
 import os
 
@@ -23,6 +26,7 @@ import pytest
 
 import oracle as O
 from nutllm_amd import workloads as W
+from screening import screen_twin
 
 pytestmark = pytest.mark.gpu
 
@@ -175,6 +179,48 @@ def test_llama7b_widths_token_kernel_vs_oracle(gpu):
         om.reset()
         ref, _, _ = om.generate(prompt, 8)
         assert ids == ref
+    finally:
+        dev.set_path(gpu.PATH_AUTO)
+        dev.close()
+
+
+@pytest.mark.parametrize("case", ["twin-up-next", "twin-down-lower-wg", "nan-top"])
+def test_llama7b_widths_screened_argmax(gpu, case):
+    """The wide kernel's screened classifier argmax (dim 4096) on rows whose
+    INT8 screening copy equals the argmax row's with an fp32 logit about
+    0.1 higher (the twin one row later) or lower (the twin 700 rows
+    earlier), and on a NaN weight in the argmax row: the greedy ids equal
+    the oracle's on the same weights."""
+    O.orc().orc_set_threads(16)
+    model = W.build("llama7b_2l", 1, 4, norm_seed=13)
+    c = model.config
+    prompt = gpu.synth_tokens(7, c.vocab_size, 20)
+    om = O.oracle_model(model)
+    hidden = np.asarray(om.prefill(prompt), np.float64)
+    top = int(np.argmax(om.logits(hidden)))
+    x = hidden / np.sqrt(np.mean(hidden * hidden) + 1e-5) * model.final_norm
+    head = model.lm_head.copy()
+    if case == "nan-top":
+        assert top != 0  # a NaN at row 0 would be the scan's answer
+        head[top, 5] = np.nan
+    else:
+        up = case == "twin-up-next"
+        other = (top + (1 if up else -700)) % c.vocab_size
+        head[other] = screen_twin(head[top], x, up)
+    dev = model.to_device()
+    try:
+        dev.set_globals(model.embeddings, model.final_norm, head)
+        dev.set_path(gpu.PATH_TOKEN)
+        ids, _ = dev.generate(prompt, 4)
+        changed = dataclasses.replace(model, lm_head=head)  # layer norms kept
+        ref, _, _ = O.oracle_model(changed).generate(prompt, 4)
+        assert ids == ref, (ids, ref, top)
+        if case == "nan-top":
+            assert ids[0] != top
+        elif case == "twin-up-next":
+            assert ids[0] == (top + 1) % c.vocab_size
+        else:
+            assert ids[0] == top
     finally:
         dev.set_path(gpu.PATH_AUTO)
         dev.close()

@@ -19,6 +19,7 @@
   to the value the reference computed for the same model.
 * The token kernel's exchange tags across a restart of their 32-bit range.
 """
+import dataclasses
 import json
 import os
 
@@ -27,6 +28,7 @@ import pytest
 
 import oracle as O
 from nutllm_amd import workloads as W
+from screening import screen_twin
 
 pytestmark = pytest.mark.gpu
 
@@ -176,44 +178,12 @@ def test_argmax_first_index_on_device_ties(gpu, tie_model, path, offset):
         dev.set_path(path)
         ids, _ = dev.generate(prompt, 4)
         assert ids[0] == min(top, other), (ids, top, other)
-        tied = W.SynthModel(model.config, model.qtype, model.seed,
-                            model.embeddings, model.final_norm, head,
-                            model.layers)
+        tied = dataclasses.replace(model, lm_head=head)
         ref, _, _ = O.oracle_model(tied).generate(prompt, 4)
         assert ids == ref
     finally:
         dev.set_path(0)
         dev.set_globals(model.embeddings, model.final_norm, model.lm_head)
-
-
-def screen_scales(row):
-    """Block-32 scales of the screening copy: the smallest fp16 at or above
-    each block's max |w| / 127."""
-    t = np.max(np.abs(row.reshape(-1, 32).astype(np.float64)), axis=1) / 127.0
-    h = t.astype(np.float16)
-    low = h.astype(np.float64) < t
-    h[low] = np.nextafter(h[low], np.float16(np.inf))
-    return h.astype(np.float64)
-
-
-def screen_twin(row, x, up):
-    """A copy of classifier row `row` whose INT8 screening copy (block-32
-    codes rint(w / s), s = screen_scales) is identical to the row's: every
-    weight but each block's largest moves half way to the edge of its code's
-    rounding interval, towards larger logits (up) or smaller ones."""
-    row = np.asarray(row, np.float32)
-    s = np.repeat(screen_scales(row), 32)
-    q = np.rint(row / s)
-    big = np.zeros(row.size, bool)
-    big[np.argmax(np.abs(row.reshape(-1, 32)), axis=1) + 32 * np.arange(row.size // 32)] = True
-    toward = np.where((x > 0) == up, 1.0, -1.0)
-    edge = (q + 0.5 * toward) * s
-    twin = np.where(big, row, (row + 0.5 * (edge - row)).astype(np.float32)).astype(np.float32)
-    keep = np.abs(twin) >= np.repeat(np.max(np.abs(row.reshape(-1, 32)), axis=1), 32)
-    twin[keep & ~big] = row[keep & ~big]  # no block maximum changes
-    assert np.array_equal(screen_scales(twin), screen_scales(row))
-    assert np.array_equal(np.rint(twin / s), q)
-    return twin
 
 
 @pytest.mark.parametrize("offset,up", [(1, True), (700, True), (-1, False), (-700, False)],
@@ -241,9 +211,7 @@ def test_argmax_screen_near_ties(gpu, tie_model, path, offset, up):
         dev.set_path(path)
         ids, _ = dev.generate(prompt, 4)
         assert ids[0] == want, (ids, top, other, gap)
-        twin = W.SynthModel(model.config, model.qtype, model.seed,
-                            model.embeddings, model.final_norm, head,
-                            model.layers)
+        twin = dataclasses.replace(model, lm_head=head)
         ref, _, _ = O.oracle_model(twin).generate(prompt, 4)
         assert ids == ref
     finally:
@@ -274,9 +242,7 @@ def test_argmax_nonfinite_classifier_rows(gpu, tie_model, path, poison):
     try:
         dev.set_path(path)
         ids, _ = dev.generate(prompt, 4)
-        bad = W.SynthModel(model.config, model.qtype, model.seed,
-                           model.embeddings, model.final_norm, head,
-                           model.layers)
+        bad = dataclasses.replace(model, lm_head=head)
         ref, _, _ = O.oracle_model(bad).generate(prompt, 4)
         assert ids == ref, (ids, ref, top)
         if poison == "nan-top":
