@@ -376,8 +376,8 @@ __global__ __launch_bounds__(kThreads) void pick_token_kernel(
 
 // The screening copy of the fp32 classifier as INT8 block-32 codes, one
 // thread per (row, block): the scale s = the smallest fp16 >= max|w| / 127
-// (so no code needs clamping and |w - s q| <= s / 2), q = rint(w / s) in
-// double. A block with a non-finite weight gets a NaN scale (its rows
+// and >= 2^-14 (so no code needs clamping, |w - s q| <= s / 2, and no
+// scale is subnormal), q = rint(w / s) in double. A block with a non-finite weight gets a NaN scale (its rows
 // always stay candidates), an all-zero block s = 0.
 __global__ __launch_bounds__(kThreads) void classifier_screen_kernel(
     const float *w, int vocab, int dim, int8_t *codes, uint16_t *scales)
@@ -412,6 +412,8 @@ __global__ __launch_bounds__(kThreads) void classifier_screen_kernel(
         bits = __builtin_bit_cast(uint16_t, _Float16(float(t)));
         if (double(__builtin_bit_cast(_Float16, bits)) < t)
             bits++; // the next fp16 up (t > 0)
+        // never a subnormal scale (a flush to zero would void the bound)
+        bits = bits < 0x0400u ? uint16_t(0x0400u) : bits;
         // w / s as w * (1 / s) in double: off the exact quotient by far
         // less than the 2^-10 s the bound allows beyond s / 2
         inv = 1.0 / double(__builtin_bit_cast(_Float16, bits));

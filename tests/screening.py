@@ -7,12 +7,12 @@ import numpy as np
 
 def screen_scales(row):
     """Block-32 scales of the screening copy: the smallest fp16 at or above
-    each block's max |w| / 127."""
+    each block's max |w| / 127, and at least 2^-14."""
     t = np.max(np.abs(row.reshape(-1, 32).astype(np.float64)), axis=1) / 127.0
     h = t.astype(np.float16)
     low = h.astype(np.float64) < t
     h[low] = np.nextafter(h[low], np.float16(np.inf))
-    return h.astype(np.float64)
+    return np.maximum(h.astype(np.float64), 2.0 ** -14)
 
 
 def screen_twin(row, x, up):
