@@ -9,10 +9,12 @@
 // and, when generating, the final rmsnorm + fp32 classifier + first-index
 // argmax (src/generate.cpp:195-207) before each decode step.
 //
-// Phases exchange activations through HBM as 64-bit (value, tag) words
-// written with agent-scope (sc1) stores; a consumer polls the words it needs
-// until they carry the producing phase's tag, so the flag is the data itself
-// and no cache-wide writeback or invalidate is needed.
+// Phases exchange activations through HBM in words written with agent-scope
+// (sc1) stores; a consumer polls the words it needs until they hold the
+// producing phase's output, so the flag is the data itself and no cache-wide
+// writeback or invalidate is needed. With the fused attention every exchange
+// of a launch has write-once 32-bit words of its own (unset until written);
+// split attention reuses its words with 64-bit (value, tag) words.
 //
 // Latency hiding: before a workgroup waits for a phase's input, it starts
 // LDS DMA (global_load_lds_dwordx4) of that phase's weight rows — and, for
@@ -82,10 +84,20 @@ struct Geo {
     static constexpr int W_GU = ROWS_GU * (RB_DIM + SB_DIM);
     static constexpr int W_DN = ROWS_DN * (RB_FFN + SB_FFN);
     static constexpr int W_WO = ROWS_WO * (RB_DIM + SB_DIM);
+    // Fused attention by KV head group: group g (KV head g) owns the q rows
+    // of its GROUP query heads, then its k and v rows (GR rows), over the
+    // WGS_G workgroups of the group, GR_WG rows each; and the Wo partial
+    // sums over its GQ context columns, WO_WG rows per workgroup (WO_SEG
+    // bytes and WO_BLK blocks of each row).
+    static constexpr int GQ = GROUP * HD, GR = GQ + 2 * HD;
+    static constexpr int WGS_G = kGrid / KVH;
+    static constexpr int GR_WG = GR / WGS_G, WO_WG = DIM / WGS_G;
+    static constexpr int WO_SEG = RB_DIM / KVH, WO_BLK = BLK_DIM / KVH;
+    static constexpr int W_WO_G = WO_WG * (WO_SEG + 2 * WO_BLK);
     // region 1 holds, in turn, the K/V staging (packed by the live position
     // count) and the QKV, gate/up and W2 rows of a phase
     static constexpr int R1 = cmax(cmax(KV_BYTES, W_QKV), cmax(W_GU, W_DN));
-    static constexpr int R2 = W_WO;
+    static constexpr int R2 = cmax(W_WO, W_WO_G);
     // Split attention for long contexts: workgroup b takes KV head
     // b / SPLITS and the b % SPLITS-th run of at most PMAX positions.
     static constexpr int SPLITS = kGrid / KVH;
@@ -104,6 +116,13 @@ struct Geo {
     static_assert(HD == 64 && HPW * (HD / 4) == kWave && GROUP % HPW == 0,
                   "attention: 16 lanes per head row, a wave's heads share a kv head");
     static_assert((DIM + 2 * KVD) % 2 == 0 && KVD % 2 == 0, "row pairs");
+    static_assert(KVH == 4 && GR % WGS_G == 0 && GR_WG % 2 == 0 && GR_WG <= ROWS_QKV &&
+                      GR_WG / 2 <= kWaves && GQ % HD == 0,
+                  "fused attention: a KV head's q/k/v row pairs over two XCDs' workgroups");
+    static_assert(GROUP == kWaves && HD == kWave && NP <= kWave && GQ / 4 <= kThreads,
+                  "fused attention: a wave per query head, a lane per dim and per position");
+    static_assert(DIM % WGS_G == 0 && WO_BLK == 16 && WO_WG == 4 * kWaves && WO_SEG % 16 == 0,
+                  "fused attention Wo: four rows of 16 blocks per wave");
 };
 
 // ------------------------------------------------- split attention --
@@ -240,6 +259,26 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
     }
 }
 
+// LDS DMA of `rows` segments of `seg` bytes (a multiple of 16), row r at
+// src + r * stride, packed in LDS (segment r at lds_dst + r * seg); issued
+// as dma() is, with the same completion.
+__device__ __forceinline__ void dma_segments(uint8_t *lds_dst, const uint8_t *src, int rows,
+                                             int seg, int stride)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int per = seg >> 4; // granules per segment
+    const int instrs = (rows * per + kWave - 1) / kWave;
+    for (int i = wave_index(); i < instrs; i += kWaves) {
+        const int k = i * kWave + lane, row = k / per, g = k - row * per;
+        if (row < rows)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(src + size_t(row) * stride +
+                                                                 g * 16),
+                (__attribute__((address_space(3))) void *)(lds_dst + i * 1024), 16, 0,
+                kStreamPolicy);
+    }
+}
+
 // ------------------------------------------------------------- kernel --
 
 template <class G> struct Lds {
@@ -302,6 +341,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     wg_share(G::DIM, wo_b, wo_e);
     wg_share(G::FFN, gu_b, gu_e); // (gate, up) pairs
     wg_share(G::DIM, dn_b, dn_e);
+    // Fused attention: KV head group grp of this workgroup (its workgroups
+    // sit on XCDs 2 grp and 2 grp + 1 under round-robin dispatch) and its
+    // index gj in the group.
+    const int grp = (blockIdx.x & 7) >> 1;
+    const int gj = ((blockIdx.x >> 3) << 1) | (blockIdx.x & 1);
 
     // Weight staging of each phase (region and slot layout). Weights are
     // addressed from the arena base alone, so staging issues no loads.
@@ -323,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 size_t(lo) * sb,
             (hi - lo) * sb);
     };
-    auto stage_qkv = [&](int layer) {
+    auto stage_qkv_all = [&](int layer) {
         const int lo = 2 * qkv_b, hi = 2 * qkv_e;
         const int q_hi = G::DIM, k_hi = G::DIM + G::KVD;
         stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 0, lo,
@@ -333,8 +377,37 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 2,
               max(lo, k_hi) - k_hi, hi - k_hi, max(lo, k_hi) - lo);
     };
+    // Fused attention: the group's rows [lo, hi) are q rows of its heads,
+    // then its k and v rows.
+    auto stage_qkv_group = [&](int layer) {
+        const int lo = gj * G::GR_WG, hi = lo + G::GR_WG;
+        const int kb = G::GQ, vb = G::GQ + G::HD;
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 0, grp * G::GQ + lo,
+              grp * G::GQ + min(hi, kb), 0);
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 1, grp * G::HD + max(lo, kb) - kb,
+              grp * G::HD + min(hi, vb) - kb, max(lo, kb) - lo);
+        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 2, grp * G::HD + max(lo, vb) - vb,
+              grp * G::HD + hi - vb, max(lo, vb) - lo);
+    };
+    auto stage_qkv = [&](int layer) {
+        if constexpr (LONG)
+            stage_qkv_all(layer);
+        else
+            stage_qkv_group(layer);
+    };
     auto stage_wo = [&](int layer) {
-        stage(r2, G::ROWS_WO, G::RB_DIM, G::SB_DIM, layer, 3, wo_b, wo_e, 0);
+        if constexpr (LONG) {
+            stage(r2, G::ROWS_WO, G::RB_DIM, G::SB_DIM, layer, 3, wo_b, wo_e, 0);
+        } else {
+            // the group's columns of rows [gj WO_WG, +WO_WG), then their scales
+            const size_t row0 = size_t(gj) * G::WO_WG;
+            dma_segments(r2, wdata(layer, 3) + row0 * G::RB_DIM + grp * G::WO_SEG, G::WO_WG,
+                         G::WO_SEG, G::RB_DIM);
+            dma_segments(r2 + G::WO_WG * G::WO_SEG,
+                         reinterpret_cast<const uint8_t *>(wscales(layer, 3)) +
+                             row0 * G::SB_DIM + grp * 2 * G::WO_BLK,
+                         G::WO_WG, 2 * G::WO_BLK, G::SB_DIM);
+        }
     };
     auto stage_gu = [&](int layer) {
         stage(r1, G::ROWS_GU, G::RB_DIM, G::SB_DIM, layer, 4, gu_b, gu_e, 0);
@@ -355,9 +428,23 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         sc = reinterpret_cast<const uint16_t *>(region + rows * rb + s * sb);
     };
 
+    // Fused attention: each layer's exchanges in write-once words of their
+    // own (q/k/v, h after Wo, act, h after W2); split attention keeps the
+    // tagged words.
+    // (q/k/v by group: group g's GR rows at g GR; the Wo partial sums of
+    // group g at ON_WO + g DIM)
+    constexpr int ON_WO = G::DIM + 2 * G::KVD, ON_GU = ON_WO + G::KVH * G::DIM;
+    constexpr int ON_DN = ON_GU + G::FFN;
+    constexpr int ONCE = ON_DN + G::DIM;
+    auto once = [&](int it, int layer, int part) {
+        return a.x_once + (size_t(it) * a.layer_count + layer) * ONCE + part;
+    };
+
     int count = 0, done = 0, last_token = 0;
     // Tag of the hidden state the next classifier reads; 0 = hidden_in.
     unsigned hidden_tag = 0;
+    // The same hidden state's write-once words (fused attention).
+    const float *hidden_once = nullptr;
     // Each phase's weight rows (and attention's K/V rows) are issued just
     // before the wait for its input. Measured: issuing them a phase earlier
     // puts the bulk reads inside other workgroups' exchange waits or under
@@ -377,8 +464,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 h.load(a.hidden_in);
                 sq = h.store(h_raw);
                 __syncthreads();
-            } else {
+            } else if constexpr (LONG) {
                 sq = take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
+            } else {
+                sq = take_once<G::DIM, false>(hidden_once, h_raw, error);
             }
             const float scale = rms_scale(wg_sum(sq, red), G::DIM);
             // x in plain layout (lane needs x[4c..4c+3], c = lane + 64 j) in
@@ -431,12 +520,32 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // ---------------------------------------------- phase A: qkv --
             // RoPE factors of this wave's first pair, read before the wait.
+            // Pair `pair` of this workgroup: its first row's index in the
+            // exchange, which matrix (q, k, v), its dim d and its KV head.
+            const int npairs = LONG ? qkv_e - qkv_b : G::GR_WG / 2;
+            auto qkv_row = [&](int pair, int &xrow, int &which, int &d, int &kvh) {
+                if constexpr (LONG) {
+                    const int row = 2 * (qkv_b + pair);
+                    which = row < G::DIM ? 0 : row < G::DIM + G::KVD ? 1 : 2;
+                    const int local = which == 0 ? row : which == 1 ? row - G::DIM
+                                                                    : row - G::DIM - G::KVD;
+                    kvh = local / G::HD;
+                    d = local % G::HD;
+                    xrow = row;
+                } else {
+                    const int lr = gj * G::GR_WG + 2 * pair;
+                    which = lr < G::GQ ? 0 : lr < G::GQ + G::HD ? 1 : 2;
+                    d = lr % G::HD;
+                    kvh = grp;
+                    xrow = grp * G::GR + lr;
+                }
+            };
             float2 rope_cs = make_float2(1.0f, 0.0f);
-            if (wave < qkv_e - qkv_b) {
-                const int row = 2 * (qkv_b + wave);
-                const int local = row < G::DIM ? row : row - G::DIM;
-                if (row < G::DIM + G::KVD)
-                    rope_cs = a.rope[size_t(pos) * (G::HD / 2) + (local % G::HD) / 2];
+            if (wave < npairs) {
+                int xrow, which, d, kvh;
+                qkv_row(wave, xrow, which, d, kvh);
+                if (which < 2)
+                    rope_cs = a.rope[size_t(pos) * (G::HD / 2) + d / 2];
             }
             // this thread's quartet of the norm weights (stage_x)
             float4 nw4 = reinterpret_cast<const float4 *>(norm(l, false))[threadIdx.x];
@@ -446,16 +555,18 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 e.load(a.embeddings + size_t(token) * G::DIM);
                 sq = e.store(h_raw);
                 dma_wait();
-            } else {
+            } else if constexpr (LONG) {
                 sq = take<G::DIM, false, false, PollDelay<LONG>::A>(a.x_hidden, h_raw, tag - 1, error);
+            } else {
+                sq = take_once<G::DIM, false, PollDelay<LONG>::A>(once(it, l - 1, ON_DN), h_raw,
+                                                                   error);
             }
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 2 + 13 * l);
             {
                 XDigits<G::CPL_DIM> x;
                 load_x(x, xl, xsc, G::BLK_DIM);
-                for (int pair = wave; pair < qkv_e - qkv_b; pair += kWaves) {
-                    const int row = 2 * (qkv_b + pair);
+                for (int pair = wave; pair < npairs; pair += kWaves) {
                     const uint8_t *d0, *d1;
                     const uint16_t *s0, *s1;
                     slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, 2 * pair, d0, s0, r1);
@@ -463,10 +574,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     float e0 = row_dot<G::QT>(d0, s0, x, G::BLK_DIM);
                     float e1 = row_dot<G::QT>(d1, s1, x, G::BLK_DIM);
                     if (lane == 0) {
-                        const int which = row < G::DIM ? 0 : row < G::DIM + G::KVD ? 1 : 2;
-                        const int local = which == 0 ? row : which == 1 ? row - G::DIM
-                                                                        : row - G::DIM - G::KVD;
-                        const int head = local / G::HD, d = local % G::HD;
+                        int row, which, d, head;
+                        qkv_row(pair, row, which, d, head);
                         if (which < 2) {
                             const float2 cs = pair == wave ? rope_cs
                                 : a.rope[size_t(pos) * (G::HD / 2) + d / 2];
@@ -474,8 +583,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                             e0 = fmaf(even, cs.x, -(odd * cs.y));
                             e1 = fmaf(even, cs.y, odd * cs.x);
                         }
-                        put(a.x_qkv + row, e0, tag);
-                        put(a.x_qkv + row + 1, e1, tag);
+                        if constexpr (LONG) {
+                            put(a.x_qkv + row, e0, tag);
+                            put(a.x_qkv + row + 1, e1, tag);
+                        } else {
+                            put_once(once(it, l, 0) + row, e0);
+                            put_once(once(it, l, 0) + row + 1, e1);
+                        }
                         if (which > 0) {
                             float *cache = (which == 1 ? kc : vc) +
                                            (size_t(head) * a.max_seq + pos) * G::HD + d;
@@ -497,7 +611,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             const int per = cdiv(n, G::SPLITS);
             const int ap0 = min(n, int(blockIdx.x % G::SPLITS) * per);
             const int ap1 = min(n, ap0 + per);
-            float *vst = LONG ? kst + G::PMAX * G::KROW : kst + G::KVH * n * G::KROW;
+            // fused: the group's KV head only, K rows [n][KROW] then V rows
+            float *vst = LONG ? kst + G::PMAX * G::KROW : kst + n * G::KROW;
             if (LONG) {
                 const int hist = max(0, min(ap1, pos) - ap0); // rows already cached
                 if (hist > 0) {
@@ -506,12 +621,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     dma_padded_rows<kStreamPolicy>(vst, vc + row0 * G::HD, hist);
                 }
             } else if (pos > 0) {
-                for (int kvh = 0; kvh < G::KVH; kvh++) {
-                    dma_padded_rows(kst + kvh * n * G::KROW,
-                                    kc + size_t(kvh) * a.max_seq * G::HD, pos);
-                    dma_padded_rows(vst + kvh * n * G::KROW,
-                                    vc + size_t(kvh) * a.max_seq * G::HD, pos);
-                }
+                dma_padded_rows(kst, kc + size_t(grp) * a.max_seq * G::HD, pos);
+                dma_padded_rows(vst, vc + size_t(grp) * a.max_seq * G::HD, pos);
             }
             stage_wo(l);
             mark(it, 4 + 13 * l);
@@ -519,7 +630,12 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
-            take<G::DIM + 2 * G::KVD, false, false, PollDelay<LONG>::B>(a.x_qkv, qkv, tag - 1, error);
+            if constexpr (LONG)
+                take<G::DIM + 2 * G::KVD, false, false, PollDelay<LONG>::B>(a.x_qkv, qkv, tag - 1,
+                                                                            error);
+            else
+                take_once<G::GR, false, PollDelay<LONG>::B>(once(it, l, 0) + grp * G::GR, qkv,
+                                                            error);
             if (LONG) {
                 // the new position's K/V row, when it falls in this unit
                 if (pos >= ap0 && pos < ap1)
@@ -529,11 +645,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                             qkv[G::DIM + which * G::KVD + ag * G::HD + d];
                     }
             } else {
-                for (int i = threadIdx.x; i < 2 * G::KVD; i += kThreads) {
-                    const int which = i >= G::KVD;
-                    const int j = i - which * G::KVD;
-                    const int kvh = j / G::HD, d = j - kvh * G::HD;
-                    (which ? vst : kst)[(kvh * n + pos) * G::KROW + d] = qkv[G::DIM + i];
+                // qkv holds the group's q rows, then its k and v rows
+                for (int i = threadIdx.x; i < 2 * G::HD; i += kThreads) {
+                    const int which = i >= G::HD, d = i - which * G::HD;
+                    (which ? vst : kst)[pos * G::KROW + d] = qkv[G::GQ + i];
                 }
             }
 
@@ -547,112 +662,80 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 quartet_digits<G::QT>(reinterpret_cast<const float4 *>(qkv)[threadIdx.x],
                                       threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             } else {
-                // Wave w: query heads 4w..4w+3, all of kv head 4w / GROUP.
-                // Lane (hh = lane / 16, r = lane % 16): scores of head hh at
-                // positions r, r + 16, ...; then context quad r of head hh.
-                constexpr int PASSES = cdiv(G::NP, 16);
-                const int hh = lane >> 4, r = lane & 15;
-                const int head = wave * G::HPW + hh;
-                const int g = (wave * G::HPW) / G::GROUP;
-                const float *kg = kst + g * n * G::KROW;
-                const float *vg = vst + g * n * G::KROW;
-                // lane r holds dims 4r..4r+3 of q; each product takes dims
-                // 4j..4j+3 from lane j of the row by DPP broadcast (no LDS
-                // reads of q), so every lane of the wave runs the dot, a
-                // lane past n on the last row's K
-                const float4 qv = reinterpret_cast<const float4 *>(qkv + head * G::HD)[r];
-                float *sc = scores + head * G::NP;
-                float s[PASSES];
-                float m = -INFINITY;
-#pragma unroll
-                for (int ps = 0; ps < PASSES; ps++) {
-                    s[ps] = -INFINITY;
-                    if (ps * 16 < n) {
-                        const int p = ps * 16 + r;
-                        const float4 *k4 =
-                            reinterpret_cast<const float4 *>(kg + min(p, n - 1) * G::KROW);
-                        float a0 = 0.0f, a1 = 0.0f;
-                        fma_row_bcast2<0>(a0, a1, qv, k4[0], k4[1]);
-                        fma_row_bcast2<2>(a0, a1, qv, k4[2], k4[3]);
-                        fma_row_bcast2<4>(a0, a1, qv, k4[4], k4[5]);
-                        fma_row_bcast2<6>(a0, a1, qv, k4[6], k4[7]);
-                        fma_row_bcast2<8>(a0, a1, qv, k4[8], k4[9]);
-                        fma_row_bcast2<10>(a0, a1, qv, k4[10], k4[11]);
-                        fma_row_bcast2<12>(a0, a1, qv, k4[12], k4[13]);
-                        fma_row_bcast2<14>(a0, a1, qv, k4[14], k4[15]);
-                        if (p < n)
-                            s[ps] = (a0 + a1) * a.attn_scale;
-                        m = fmaxf(m, s[ps]);
-                    }
-                }
-                m = row16_max(m);
-                float total = 0.0f;
-#pragma unroll
-                for (int ps = 0; ps < PASSES; ps++) {
-                    if (ps * 16 < n) {
-                        const int p = ps * 16 + r;
-                        if (p < n) {
-                            const float e = expf(s[ps] - m);
-                            sc[p] = e;
-                            total += e;
-                        }
-                    }
-                }
-                total = row16_sum(total);
-                // context: lanes of head hh own quad r of its output row
-                // (even and odd positions in two accumulators, eight
-                // positions' loads in flight)
-                const float4 *v4 = reinterpret_cast<const float4 *>(vg) + r;
-                float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                float4 acc1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                // Wave w: query head w of the group. Lane p scores position
+                // p, its K row from LDS and q's dims 4j..4j+3 from lane j of
+                // its 16-lane row by DPP broadcast (every lane runs the dot,
+                // lanes past n on the last row); then lane d sums context dim
+                // d over the positions, their weights by readlane.
+                const float4 qv = reinterpret_cast<const float4 *>(qkv + wave * G::HD)[lane & 15];
+                const float4 *k4 =
+                    reinterpret_cast<const float4 *>(kst + min(lane, n - 1) * G::KROW);
+                float a0 = 0.0f, a1 = 0.0f;
+                fma_row_bcast2<0>(a0, a1, qv, k4[0], k4[1]);
+                fma_row_bcast2<2>(a0, a1, qv, k4[2], k4[3]);
+                fma_row_bcast2<4>(a0, a1, qv, k4[4], k4[5]);
+                fma_row_bcast2<6>(a0, a1, qv, k4[6], k4[7]);
+                fma_row_bcast2<8>(a0, a1, qv, k4[8], k4[9]);
+                fma_row_bcast2<10>(a0, a1, qv, k4[10], k4[11]);
+                fma_row_bcast2<12>(a0, a1, qv, k4[12], k4[13]);
+                fma_row_bcast2<14>(a0, a1, qv, k4[14], k4[15]);
+                const float sc = lane < n ? (a0 + a1) * a.attn_scale : -INFINITY;
+                const float m = wave_maximum(sc);
+                const float e = lane < n ? expf(sc - m) : 0.0f;
+                const float total = wave_total(e);
+                const float *vcol = vst + lane;
+                auto weight = [&](int q) {
+                    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), q));
+                };
+                float c0 = 0.0f, c1 = 0.0f;
                 int p = 0;
                 for (; p + 8 <= n; p += 8) {
-                    float4 v[8];
-                    float w[8];
+                    float v[8];
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        v[j] = v4[(p + j) * (G::KROW / 4)];
-                        w[j] = sc[p + j];
-                    }
+                    for (int j = 0; j < 8; j++)
+                        v[j] = vcol[(p + j) * G::KROW];
 #pragma unroll
                     for (int j = 0; j < 8; j += 2) {
-                        acc.x = fmaf(w[j], v[j].x, acc.x);
-                        acc.y = fmaf(w[j], v[j].y, acc.y);
-                        acc.z = fmaf(w[j], v[j].z, acc.z);
-                        acc.w = fmaf(w[j], v[j].w, acc.w);
-                        acc1.x = fmaf(w[j + 1], v[j + 1].x, acc1.x);
-                        acc1.y = fmaf(w[j + 1], v[j + 1].y, acc1.y);
-                        acc1.z = fmaf(w[j + 1], v[j + 1].z, acc1.z);
-                        acc1.w = fmaf(w[j + 1], v[j + 1].w, acc1.w);
+                        c0 = fmaf(weight(p + j), v[j], c0);
+                        c1 = fmaf(weight(p + j + 1), v[j + 1], c1);
                     }
                 }
-                for (; p < n; p++) {
-                    const float4 v = v4[p * (G::KROW / 4)];
-                    const float w = sc[p];
-                    acc.x = fmaf(w, v.x, acc.x);
-                    acc.y = fmaf(w, v.y, acc.y);
-                    acc.z = fmaf(w, v.z, acc.z);
-                    acc.w = fmaf(w, v.w, acc.w);
-                }
-                acc.x += acc1.x;
-                acc.y += acc1.y;
-                acc.z += acc1.z;
-                acc.w += acc1.w;
-                const float inv = 1.0f / total;
-                const int e0 = head * G::HD + 4 * r;
-                quartet_digits<G::QT>(make_float4(acc.x * inv, acc.y * inv, acc.z * inv,
-                                                  acc.w * inv),
-                                      e0 >> 5, (e0 >> 2) & 7, xl, xsc);
+                for (; p < n; p++)
+                    c0 = fmaf(weight(p), vcol[p * G::KROW], c0);
+                // the group's context (GQ values) over the scores region
+                scores[wave * G::HD + lane] = (c0 + c1) * (1.0f / total);
+                __syncthreads();
+                // as digits, one quartet per thread of the first GQ / 4
+                if (threadIdx.x < G::GQ / 4)
+                    quartet_digits<G::QT>(reinterpret_cast<const float4 *>(scores)[threadIdx.x],
+                                          threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             }
             __syncthreads();
             mark(it, 6 + 13 * l);
-            for (int r = wave; r < wo_e - wo_b; r += kWaves) {
-                const uint8_t *d;
-                const uint16_t *s;
-                slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
-                const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xl, xsc, G::BLK_DIM);
-                if (lane == 0)
-                    put(a.x_hidden + wo_b + r, h_raw[wo_b + r] + y, tag);
+            if constexpr (LONG) {
+                for (int r = wave; r < wo_e - wo_b; r += kWaves) {
+                    const uint8_t *d;
+                    const uint16_t *s;
+                    slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
+                    const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xl, xsc, G::BLK_DIM);
+                    if (lane == 0)
+                        put(a.x_hidden + wo_b + r, h_raw[wo_b + r] + y, tag);
+                }
+            } else {
+                // Wo partial sums over the group's context columns: wave w
+                // takes rows 4 w .. 4 w + 3 of this workgroup's, a row of 16
+                // lanes each, lane b one block; the residual is added by the
+                // consumers
+                const int r = 4 * wave + (lane >> 4), b = lane & 15;
+                const uint8_t *d = r2 + r * G::WO_SEG;
+                const uint16_t *s = reinterpret_cast<const uint16_t *>(
+                    r2 + G::WO_WG * G::WO_SEG + r * 2 * G::WO_BLK);
+                uint4 dg[6];
+                load_digits(xl, b, dg);
+                const float y = row16_sum(half_bits_to_float(s[b]) * xsc[b] *
+                                          dot_block_digits<G::QT>(d, b, dg));
+                if (b == 0)
+                    put_once(once(it, l, ON_WO) + grp * G::DIM + gj * G::WO_WG + r, y);
             }
             tag++;
             // every wave is past attention (region 1) and past its reads of
@@ -664,7 +747,12 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
-            sq = take<G::DIM, false, false, PollDelay<LONG>::C>(a.x_hidden, h_raw, tag - 1, error);
+            if constexpr (LONG)
+                sq = take<G::DIM, false, false, PollDelay<LONG>::C>(a.x_hidden, h_raw, tag - 1,
+                                                                    error);
+            else
+                sq = take_once_sum<G::DIM, G::KVH, PollDelay<LONG>::C>(once(it, l, ON_WO), h_raw,
+                                                                      error);
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 9 + 13 * l);
             {
@@ -677,8 +765,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, G::ROWS_GU / 2 + pair, du, su, r1);
                     const float g = row_dot<G::QT>(dg, sg, x, G::BLK_DIM);
                     const float u = row_dot<G::QT>(du, su, x, G::BLK_DIM);
-                    if (lane == 0)
-                        put(a.x_act + gu_b + pair, g / (1.0f + expf(-g)) * u, tag);
+                    if (lane == 0) {
+                        const float act = g / (1.0f + expf(-g)) * u;
+                        if constexpr (LONG)
+                            put(a.x_act + gu_b + pair, act, tag);
+                        else
+                            put_once(once(it, l, ON_GU) + gu_b + pair, act);
+                    }
                 }
             }
             tag++;
@@ -688,7 +781,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
-            take<G::FFN, true, false, PollDelay<LONG>::D>(a.x_act, xs, tag - 1, error);
+            if constexpr (LONG)
+                take<G::FFN, true, false, PollDelay<LONG>::D>(a.x_act, xs, tag - 1, error);
+            else
+                take_once<G::FFN, true, PollDelay<LONG>::D>(once(it, l, ON_GU), xs, error);
             block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {
@@ -700,7 +796,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const float y = row_dot_floats<G::QT, G::CPL_FFN>(d, s, xs, xsc, G::BLK_FFN);
                     if (lane == 0) {
                         const float v = h_raw[dn_b + r] + y;
-                        put(a.x_hidden + dn_b + r, v, tag);
+                        if constexpr (LONG)
+                            put(a.x_hidden + dn_b + r, v, tag);
+                        else
+                            put_once(once(it, l, ON_DN) + dn_b + r, v);
                         if (last && it + 1 == a.n_iter)
                             a.hidden_out[dn_b + r] = v;
                     }
@@ -711,6 +810,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     stage_qkv(l + 1);
             }
             hidden_tag = tag;
+            if constexpr (!LONG)
+                hidden_once = once(it, l, ON_DN);
             tag++;
             mark(it, 14 + 13 * l);
         }
@@ -719,7 +820,10 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     }
     // hidden_out after an early stop (eos): the state the loop ended with
     if (done && hidden_tag != 0) {
-        take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
+        if constexpr (LONG)
+            take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
+        else
+            take_once<G::DIM, false>(hidden_once, h_raw, error);
         for (int i = threadIdx.x; i < G::DIM; i += kThreads)
             if (blockIdx.x == 0)
                 a.hidden_out[i] = h_raw[i];
@@ -774,6 +878,10 @@ void launch_as(const TokenArgs &args, hipStream_t stream)
             "token kernel: launch exceeds its exchange tag range");
     require(!LONG || (args.x_apart != nullptr && args.x_ctx != nullptr), NUT_EINVAL,
             "token kernel: split attention needs its exchange buffers");
+    require(LONG || args.x_once != nullptr, NUT_EINVAL,
+            "token kernel: fused attention needs its write-once exchange words");
+    static_assert(Lds<G>::BYTES > 0 && G::DIM % 2 == 0 && G::KVD % 2 == 0 && G::FFN % 2 == 0,
+                  "write-once words are polled in pairs");
     TokenArgs a = args;
     void *params[] = {&a};
     hip_check(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(kernel),

@@ -27,6 +27,11 @@ struct TokenArgs {
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
     uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
+    // Fused attention (long_attention == 0): the q/k/v, h and act exchanges
+    // in write-once words (token_once_floats of them, every word kUnset =
+    // 0xffffffff when the launch starts), iteration it and layer l at
+    // x_once + (it * layer_count + l) * token_once_stride.
+    float *x_once;
     // Long contexts (long_attention != 0): attention is split over the
     // workgroups; x_apart holds each workgroup's partial (m, l, o) for the
     // query heads of its KV head, x_ctx the merged context.
@@ -56,6 +61,18 @@ struct TokenArgs {
 // loop screens the classifier through its INT8 copy (TokenArgs::
 // classifier8); larger vocabularies take the plain fp32 pass.
 constexpr int kScreenRowsMax = 1024;
+
+// Write-once words per iteration and layer: q/k/v, the Wo partial sums of
+// each KV head group (h after Wo), act, h after W2.
+inline size_t token_once_stride(const DecodeShape &s)
+{
+    return size_t(s.dim) * (2 + s.kv_heads) + 2 * size_t(s.kv_heads) * s.head_dim + s.ffn_dim;
+}
+
+inline size_t token_once_floats(const DecodeShape &s, size_t layers, size_t n_iter)
+{
+    return n_iter * layers * token_once_stride(s);
+}
 
 // Exchange tags. Every exchange word is (tag << 32) | value, and a launch
 // uses the tags [base, base + 2^kTagShift) with base = count << kTagShift for

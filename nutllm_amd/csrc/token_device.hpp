@@ -47,6 +47,24 @@ __device__ __forceinline__ void put(uint64_t *p, float v, unsigned tag)
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Write-once words: an exchange that owns its words alone within a launch
+// (TokenArgs::x_once) publishes plain 32-bit values into words the host set
+// to kUnset before the launch. Each word goes from kUnset to its value once,
+// so the value is its own flag at half the bytes of a tagged word, and a
+// 64-bit poll of two words needs no atomicity across them. kUnset is a NaN
+// that put_once never writes: it publishes every NaN as the canonical one.
+constexpr uint32_t kUnset = 0xffffffffu;
+
+__device__ __forceinline__ void put_once(float *p, float v)
+{
+    store_coherent(p, v != v ? __uint_as_float(0x7fc00000u) : v);
+}
+
+__device__ __forceinline__ bool unset_pair(uint64_t w)
+{
+    return uint32_t(w) == kUnset || uint32_t(w >> 32) == kUnset;
+}
+
 __device__ __forceinline__ bool failed(const int *error)
 {
     return __hip_atomic_load(error, __ATOMIC_RELAXED,
@@ -367,6 +385,139 @@ __device__ float take(const uint64_t *src, float *dst, unsigned tag,
             const float f = __uint_as_float(unsigned(v[u]));
             dst[SWIZZLE ? swz(i) : i] = f;
             squares = fmaf(f, f, squares);
+        }
+    }
+    dma_wait();
+    return squares;
+}
+
+// take for write-once words: dst[map(i)] = src[i] once set, i < N (even,
+// src 8-byte aligned). Thread t polls the word pairs t, t + kThreads, ...
+// as 64-bit loads, re-issuing every pair that still holds kUnset; returns
+// this thread's sum of squares. Same delay, bound and closing DMA wait and
+// barrier as take.
+template <int N, bool SWIZZLE, int DELAY = 0>
+__device__ float take_once(const float *src, float *dst, int *error)
+{
+    static_assert(N % 2 == 0, "whole word pairs");
+    constexpr int PAIRS = N / 2;
+    constexpr int PER = cdiv(PAIRS, kThreads);
+    const uint64_t *src2 = reinterpret_cast<const uint64_t *>(src);
+    if (DELAY > 0) {
+        const unsigned long long until = __builtin_amdgcn_s_memrealtime() + DELAY;
+        while (__builtin_amdgcn_s_memrealtime() < until)
+            __builtin_amdgcn_s_sleep(1);
+    }
+    uint64_t v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        v[u] = i < PAIRS ? load_coherent(src2 + i) : 0;
+    }
+    for (int spins = 0;; spins++) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            stale |= unset_pair(v[u]);
+        if (!stale)
+            break;
+        if ((spins & 63) == 63 && failed(error))
+            break;
+        if (spins > kSpinLimit) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+            if (unset_pair(v[u]))
+                v[u] = load_coherent(src2 + threadIdx.x + u * kThreads);
+    }
+    float squares = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < PAIRS) {
+            const float lo = __uint_as_float(uint32_t(v[u]));
+            const float hi = __uint_as_float(uint32_t(v[u] >> 32));
+            // 2i and 2i + 1 share a quad, so they stay adjacent under swz
+            *reinterpret_cast<float2 *>(dst + (SWIZZLE ? swz(2 * i) : 2 * i)) =
+                make_float2(lo, hi);
+            squares = fmaf(lo, lo, squares);
+            squares = fmaf(hi, hi, squares);
+        }
+    }
+    dma_wait();
+    return squares;
+}
+
+// take_once of PARTS partial sums of an N-vector (part k at src + k N) onto
+// dst: dst[i] += (p_0[i] + p_1[i]) + ... in part order, the same arithmetic
+// in every workgroup; returns this thread's sum of squares of the new dst.
+template <int N, int PARTS, int DELAY = 0>
+__device__ float take_once_sum(const float *src, float *dst, int *error)
+{
+    static_assert(N % 2 == 0, "whole word pairs");
+    constexpr int PAIRS = N / 2;
+    constexpr int PER = cdiv(PAIRS, kThreads);
+    const uint64_t *src2 = reinterpret_cast<const uint64_t *>(src);
+    if (DELAY > 0) {
+        const unsigned long long until = __builtin_amdgcn_s_memrealtime() + DELAY;
+        while (__builtin_amdgcn_s_memrealtime() < until)
+            __builtin_amdgcn_s_sleep(1);
+    }
+    uint64_t v[PER][PARTS];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+#pragma unroll
+        for (int k = 0; k < PARTS; k++)
+            v[u][k] = i < PAIRS ? load_coherent(src2 + k * PAIRS + i) : 0;
+    }
+    for (int spins = 0;; spins++) {
+        bool stale = false;
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+#pragma unroll
+            for (int k = 0; k < PARTS; k++)
+                stale |= unset_pair(v[u][k]);
+        if (!stale)
+            break;
+        if ((spins & 63) == 63 && failed(error))
+            break;
+        if (spins > kSpinLimit) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < PER; u++)
+#pragma unroll
+            for (int k = 0; k < PARTS; k++)
+                if (unset_pair(v[u][k]))
+                    v[u][k] = load_coherent(src2 + k * PAIRS + threadIdx.x + u * kThreads);
+    }
+    float squares = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = threadIdx.x + u * kThreads;
+        if (i < PAIRS) {
+            float lo = __uint_as_float(uint32_t(v[u][0]));
+            float hi = __uint_as_float(uint32_t(v[u][0] >> 32));
+#pragma unroll
+            for (int k = 1; k < PARTS; k++) {
+                lo += __uint_as_float(uint32_t(v[u][k]));
+                hi += __uint_as_float(uint32_t(v[u][k] >> 32));
+            }
+            float2 *h = reinterpret_cast<float2 *>(dst + 2 * i);
+            const float2 old = *h;
+            lo += old.x;
+            hi += old.y;
+            *h = make_float2(lo, hi);
+            squares = fmaf(lo, lo, squares);
+            squares = fmaf(hi, hi, squares);
         }
     }
     dma_wait();
