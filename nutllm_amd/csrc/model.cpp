@@ -573,14 +573,15 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     // beyond the fused attention pass, attention is split over the grid
     a.long_attention =
         start + n_iter > size_t(token_kernel_max_positions(m.type, s)) ? 1 : 0;
-    if (a.long_attention == 0 && wide_kernel_positions(m.type, s) == 0) {
-        // every word of this launch's write-once exchanges unset (0xffffffff)
-        const size_t floats = token_once_floats(s, m.config.layers, n_iter);
-        const size_t cap = token_once_floats(
-            s, m.config.layers, size_t(token_kernel_max_positions(m.type, s)));
-        require(floats <= cap, NUT_EINVAL, "token kernel: launch exceeds its exchange words");
-        if (m.exchange_once.get() == nullptr)
-            m.exchange_once.allocate(cap * sizeof(float));
+    if (a.long_attention == 0) {
+        // every word of this launch's write-once exchanges unset (0xffffffff);
+        // the buffer grows to the largest launch so far
+        const bool wide = wide_kernel_positions(m.type, s) > 0;
+        const size_t floats = token_once_floats(s, wide, m.config.layers, n_iter);
+        if (floats * sizeof(float) > m.exchange_once.bytes()) {
+            m.exchange_once.release();
+            m.exchange_once.allocate(floats * sizeof(float));
+        }
         hip_check(hipMemsetAsync(m.exchange_once.get(), 0xff, floats * sizeof(float), m.stream),
                   "hipMemsetAsync");
         a.x_once = m.exchange_once.as<float>();

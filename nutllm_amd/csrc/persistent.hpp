@@ -27,9 +27,10 @@ struct TokenArgs {
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
     uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
-    // Fused attention (long_attention == 0): the q/k/v, h and act exchanges
-    // in write-once words (token_once_floats of them, every word kUnset =
-    // 0xffffffff when the launch starts), iteration it and layer l at
+    // Fused attention (long_attention == 0) and the wide kernel: the h, act
+    // and (q/k/v or context) exchanges in write-once words
+    // (token_once_floats of them, every word kUnset = 0xffffffff when the
+    // launch starts), iteration it and layer l at
     // x_once + (it * layer_count + l) * token_once_stride.
     float *x_once;
     // Long contexts (long_attention != 0): attention is split over the
@@ -62,16 +63,20 @@ struct TokenArgs {
 // classifier8); larger vocabularies take the plain fp32 pass.
 constexpr int kScreenRowsMax = 1024;
 
-// Write-once words per iteration and layer: q/k/v, the Wo partial sums of
-// each KV head group (h after Wo), act, h after W2.
-inline size_t token_once_stride(const DecodeShape &s)
+// Write-once words per iteration and layer. The fused-attention kernel:
+// q/k/v, the Wo partial sums of each KV head group (h after Wo), act, h
+// after W2. The wide kernel (wide.hip): the context, h after Wo, act, h
+// after W2.
+inline size_t token_once_stride(const DecodeShape &s, bool wide)
 {
+    if (wide)
+        return 3 * size_t(s.dim) + s.ffn_dim;
     return size_t(s.dim) * (2 + s.kv_heads) + 2 * size_t(s.kv_heads) * s.head_dim + s.ffn_dim;
 }
 
-inline size_t token_once_floats(const DecodeShape &s, size_t layers, size_t n_iter)
+inline size_t token_once_floats(const DecodeShape &s, bool wide, size_t layers, size_t n_iter)
 {
-    return n_iter * layers * token_once_stride(s);
+    return n_iter * layers * token_once_stride(s, wide);
 }
 
 // Exchange tags. Every exchange word is (tag << 32) | value, and a launch

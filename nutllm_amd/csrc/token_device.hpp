@@ -394,14 +394,15 @@ __device__ float take(const uint64_t *src, float *dst, unsigned tag,
 // take for write-once words: dst[map(i)] = src[i] once set, i < N (even,
 // src 8-byte aligned). Thread t polls the word pairs t, t + kThreads, ...
 // as 64-bit loads, re-issuing every pair that still holds kUnset; returns
-// this thread's sum of squares. Same delay, bound and closing DMA wait and
-// barrier as take.
-template <int N, bool SWIZZLE, int DELAY = 0>
+// this thread's sum of squares. Same delay, bound, FRESH and closing DMA
+// wait and barrier as take.
+template <int N, bool SWIZZLE, int DELAY = 0, bool FRESH = false>
 __device__ float take_once(const float *src, float *dst, int *error)
 {
     static_assert(N % 2 == 0, "whole word pairs");
     constexpr int PAIRS = N / 2;
     constexpr int PER = cdiv(PAIRS, kThreads);
+    const unsigned tid = FRESH ? unsigned(opaque_lane_value(threadIdx.x)) : threadIdx.x;
     const uint64_t *src2 = reinterpret_cast<const uint64_t *>(src);
     if (DELAY > 0) {
         const unsigned long long until = __builtin_amdgcn_s_memrealtime() + DELAY;
@@ -411,7 +412,7 @@ __device__ float take_once(const float *src, float *dst, int *error)
     uint64_t v[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++) {
-        const int i = threadIdx.x + u * kThreads;
+        const int i = tid + u * kThreads;
         v[u] = i < PAIRS ? load_coherent(src2 + i) : 0;
     }
     for (int spins = 0;; spins++) {
@@ -432,12 +433,12 @@ __device__ float take_once(const float *src, float *dst, int *error)
 #pragma unroll
         for (int u = 0; u < PER; u++)
             if (unset_pair(v[u]))
-                v[u] = load_coherent(src2 + threadIdx.x + u * kThreads);
+                v[u] = load_coherent(src2 + tid + u * kThreads);
     }
     float squares = 0.0f;
 #pragma unroll
     for (int u = 0; u < PER; u++) {
-        const int i = threadIdx.x + u * kThreads;
+        const int i = tid + u * kThreads;
         if (i < PAIRS) {
             const float lo = __uint_as_float(uint32_t(v[u]));
             const float hi = __uint_as_float(uint32_t(v[u] >> 32));

@@ -467,9 +467,19 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
         load_quartets(nw, norm(layer, false));
     };
 
+    // Write-once exchange words of iteration it, layer l: the context, h
+    // after Wo, act, h after W2 (the partial scores stay tagged).
+    constexpr int X_WO = G::DIM, X_ACT = 2 * G::DIM, X_DN = 2 * G::DIM + G::FFN;
+    constexpr int X_STRIDE = X_DN + G::DIM;
+    auto once = [&](int it, int layer, int part) {
+        return fresh(a.x_once) + (size_t(it) * a.layer_count + layer) * X_STRIDE + part;
+    };
+
     int count = 0, done = 0, last_token = 0;
     // Tag of the hidden state the next classifier reads; 0 = hidden_in.
     unsigned hidden_tag = 0;
+    // The same hidden state's write-once words.
+    const float *hidden_once = nullptr;
 
     for (int it = 0; it < a.n_iter && !done; it++) {
         int token;
@@ -489,7 +499,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 sq = h.store(hbuf);
                 __syncthreads();
             } else {
-                sq = take<G::DIM, false, true>(fresh(a.x_hidden), hbuf, hidden_tag, error);
+                sq = take_once<G::DIM, false, 0, true>(hidden_once, hbuf, error);
             }
             const float scale = rms_scale(wg_sum(sq, red), G::DIM);
 #pragma unroll
@@ -551,7 +561,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 sq = e.store(hbuf);
                 dma_wait();
             } else {
-                sq = take<G::DIM, false, true>(fresh(a.x_hidden), hbuf, hidden_tag, error);
+                sq = take_once<G::DIM, false, 0, true>(hidden_once, hbuf, error);
             }
             // this wave's residual inputs
             float res0 = hbuf[ra], res1 = hbuf[rb];
@@ -731,14 +741,13 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
 #pragma unroll
                 for (int w = 0; w < kWaves; w++)
                     t += ctxp[w * G::SLICE + threadIdx.x];
-                put(fresh(a.x_ctx) + qkv0 + threadIdx.x, t / total, tag);
+                put_once(once(it, l, 0) + qkv0 + threadIdx.x, t / total);
             }
             tag++;
             mark(it, 5 + 13 * l);
 
             // ------------------------------------ Wo rows + residual --
-            take<G::DIM, false, true, kWidePollDelayContext>(fresh(a.x_ctx), hbuf, tag - 1,
-                                                             error);
+            take_once<G::DIM, false, kWidePollDelayContext, true>(once(it, l, 0), hbuf, error);
             {
                 float4 ones[G::XQ];
 #pragma unroll
@@ -753,8 +762,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 res0 += y[0];
                 res1 += y[1];
                 if (lane == 0) {
-                    put(fresh(a.x_hidden) + ra, res0, tag);
-                    put(fresh(a.x_hidden) + rb, res1, tag);
+                    put_once(once(it, l, X_WO) + ra, res0);
+                    put_once(once(it, l, X_WO) + rb, res1);
                 }
             }
             tag++;
@@ -780,7 +789,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                                    wscales(5, r, G::SB_DIM));
             }
             load_quartets(nw, norm(l, true));
-            sq = take<G::DIM, false, true>(fresh(a.x_hidden), hbuf, tag - 1, error);
+            sq = take_once<G::DIM, false, 0, true>(once(it, l, X_WO), hbuf, error);
             stage_quartets<G::QT, G::XQ>(hbuf, nw, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 8 + 13 * l);
             {
@@ -790,8 +799,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 for (int i = 0; i < G::NREG; i++)
                     if (lane == 0) {
                         const float g = y[2 * i], u = y[2 * i + 1];
-                        put(fresh(a.x_act) + gu0 + G::GU_LDS + wave + kWaves * i,
-                            g / (1.0f + expf(-g)) * u, tag);
+                        put_once(once(it, l, X_ACT) + gu0 + G::GU_LDS + wave + kWaves * i,
+                                 g / (1.0f + expf(-g)) * u);
                     }
             }
             {
@@ -810,8 +819,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 for (int i = 0; i < G::NLDS; i++)
                     if (i < n_lds && lane == 0) {
                         const float g = y[2 * i], u = y[2 * i + 1];
-                        put(fresh(a.x_act) + gu0 + wave + kWaves * i, g / (1.0f + expf(-g)) * u,
-                            tag);
+                        put_once(once(it, l, X_ACT) + gu0 + wave + kWaves * i,
+                                 g / (1.0f + expf(-g)) * u);
                     }
             }
             tag++;
@@ -827,20 +836,21 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                        wscales(6, ra, G::SB_FFN));
             wd[1].load(layer_rsrc<G>(a.weights, l), wdata(6, rb, G::RB_FFN),
                        wscales(6, rb, G::SB_FFN));
-            take<G::FFN, true, true>(fresh(a.x_act), act, tag - 1, error);
+            take_once<G::FFN, true, 0, true>(once(it, l, X_ACT), act, error);
             block_sums(act, xsc, G::FFN);
             mark(it, 10 + 13 * l);
             res0 += regs_dot_floats(wd[0], act, xsc, G::BLK_FFN);
             res1 += regs_dot_floats(wd[1], act, xsc, G::BLK_FFN);
             if (lane == 0) {
-                put(fresh(a.x_hidden) + ra, res0, tag);
-                put(fresh(a.x_hidden) + rb, res1, tag);
+                put_once(once(it, l, X_DN) + ra, res0);
+                put_once(once(it, l, X_DN) + rb, res1);
                 if (last && it + 1 == a.n_iter) {
                     a.hidden_out[ra] = res0;
                     a.hidden_out[rb] = res1;
                 }
             }
             hidden_tag = tag;
+            hidden_once = once(it, l, X_DN);
             tag++;
             mark(it, 11 + 13 * l);
             // every wave is past its reads of the activation, which the next
@@ -854,7 +864,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
     }
     // hidden_out after an early stop (eos): the state the loop ended with
     if (done && hidden_tag != 0) {
-        take<G::DIM, false, true>(fresh(a.x_hidden), hbuf, hidden_tag, error);
+        take_once<G::DIM, false, 0, true>(hidden_once, hbuf, error);
         for (int i = threadIdx.x; i < G::DIM; i += kThreads)
             if (blockIdx.x == 0)
                 a.hidden_out[i] = hbuf[i];
@@ -902,6 +912,8 @@ void wide_launch_as(const TokenArgs &args, hipStream_t stream)
             NUT_EINVAL, "token kernel: context exceeds the attention pass");
     require(token_tags_needed(args.n_iter, args.layer_count) <= (1ll << kTagShift), NUT_EINVAL,
             "token kernel: launch exceeds its exchange tag range");
+    require(args.x_once != nullptr, NUT_EINVAL,
+            "token kernel: the wide kernel needs its write-once exchange words");
     require(args.x_scores != nullptr, NUT_EINVAL,
             "token kernel: head-dim attention needs its score buffer");
     TokenArgs a = args;
