@@ -573,7 +573,7 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     // beyond the fused attention pass, attention is split over the grid
     a.long_attention =
         start + n_iter > size_t(token_kernel_max_positions(m.type, s)) ? 1 : 0;
-    if (a.long_attention == 0) {
+    {
         // every word of this launch's write-once exchanges unset (0xffffffff);
         // the buffer grows to the largest launch so far
         const bool wide = wide_kernel_positions(m.type, s) > 0;

@@ -176,18 +176,19 @@ __device__ void take_words(Addr addr, float *dst, unsigned tag, int *error)
 // Attention of a long context split over the grid (src/quant_model.cpp:
 // 45-108 computes the same softmax over all positions at once). Workgroup
 // b owns KV head ag = b / SPLITS and its cnt positions [ap0, ap1) (K and V
-// rows staged at kst / vst): wave w computes, for query head w of the KV
-// head's group, the run's maximum score m, l = sum exp(s_p - m) and
+// rows staged at kst / vst, q of the group's heads at qkv): wave w
+// computes, for query head w of the KV head's group, the run's maximum
+// score m, l = sum exp(s_p - m) and
 // o = sum exp(s_p - m) V_p, published with `tag` as x_apart words
 // [b][head][o 0..HD-1, m, l]. Then workgroup b merges context values
 // 8 (b % 8) .. +7 of head b / 8 over its KV head's SPLITS runs (wave w
 // value w, lane sp run sp): M = max m, context = sum e^(m - M) o / sum
-// e^(m - M) l, published with tag + 1 into x_ctx. mb: LDS, SPLITS * 10
-// floats.
+// e^(m - M) l, published as write-once words at ctx_out. mb: LDS,
+// SPLITS * 10 floats.
 template <class G>
 __device__ void split_attention(int cnt, int ag, const float *kst, const float *vst,
                                 const float *qkv, float *scores, float *mb,
-                                const TokenArgs &a, unsigned tag, int *error)
+                                const TokenArgs &a, float *ctx_out, unsigned tag, int *error)
 {
     static_assert(G::GROUP == kWaves && G::PMAX == kWave && G::HD == kWave,
                   "split attention: a wave per query head, a lane per position and per dim");
@@ -195,8 +196,7 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
     {
         // wave w: query head w of the group; lane p: position p's score,
         // then lane d: context dim d
-        const float4 *q4 =
-            reinterpret_cast<const float4 *>(qkv + (ag * G::GROUP + wave) * G::HD);
+        const float4 *q4 = reinterpret_cast<const float4 *>(qkv + wave * G::HD);
         float sv = -INFINITY;
         if (lane < cnt) {
             const float4 *k4 = reinterpret_cast<const float4 *>(kst + lane * G::KROW);
@@ -255,7 +255,7 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
         const float total = wave_total(w * pl);
         const float c = wave_total(w * mb[lane * 10 + wave]);
         if (lane == 0)
-            put(a.x_ctx + mh * G::HD + md0 + wave, c / total, tag + 1);
+            put_once(ctx_out + mh * G::HD + md0 + wave, c / total);
     }
 }
 
@@ -336,16 +336,17 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         }
     };
 
-    int qkv_b, qkv_e, wo_b, wo_e, gu_b, gu_e, dn_b, dn_e;
-    wg_share((G::DIM + 2 * G::KVD) / 2, qkv_b, qkv_e); // row pairs
+    int wo_b, wo_e, gu_b, gu_e, dn_b, dn_e;
     wg_share(G::DIM, wo_b, wo_e);
     wg_share(G::FFN, gu_b, gu_e); // (gate, up) pairs
     wg_share(G::DIM, dn_b, dn_e);
-    // Fused attention: KV head group grp of this workgroup (its workgroups
-    // sit on XCDs 2 grp and 2 grp + 1 under round-robin dispatch) and its
-    // index gj in the group.
-    const int grp = (blockIdx.x & 7) >> 1;
-    const int gj = ((blockIdx.x >> 3) << 1) | (blockIdx.x & 1);
+    // KV head group grp of this workgroup and its index gj in the group:
+    // with the fused attention the group's workgroups sit on XCDs 2 grp and
+    // 2 grp + 1 under round-robin dispatch; with split attention group g is
+    // workgroups 64 g .. 64 g + 63, whose attention units are KV head g.
+    const int grp = LONG ? int(blockIdx.x) / G::WGS_G : (blockIdx.x & 7) >> 1;
+    const int gj = LONG ? int(blockIdx.x) % G::WGS_G
+                        : ((blockIdx.x >> 3) << 1) | (blockIdx.x & 1);
 
     // Weight staging of each phase (region and slot layout). Weights are
     // addressed from the arena base alone, so staging issues no loads.
@@ -367,18 +368,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 size_t(lo) * sb,
             (hi - lo) * sb);
     };
-    auto stage_qkv_all = [&](int layer) {
-        const int lo = 2 * qkv_b, hi = 2 * qkv_e;
-        const int q_hi = G::DIM, k_hi = G::DIM + G::KVD;
-        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 0, lo,
-              min(hi, q_hi), 0);
-        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 1,
-              max(lo, q_hi) - q_hi, min(hi, k_hi) - q_hi, max(lo, q_hi) - lo);
-        stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 2,
-              max(lo, k_hi) - k_hi, hi - k_hi, max(lo, k_hi) - lo);
-    };
-    // Fused attention: the group's rows [lo, hi) are q rows of its heads,
-    // then its k and v rows.
+    // The group's rows [lo, hi) are q rows of its heads, then its k and v
+    // rows.
     auto stage_qkv_group = [&](int layer) {
         const int lo = gj * G::GR_WG, hi = lo + G::GR_WG;
         const int kb = G::GQ, vb = G::GQ + G::HD;
@@ -389,12 +380,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         stage(r1, G::ROWS_QKV, G::RB_DIM, G::SB_DIM, layer, 2, grp * G::HD + max(lo, vb) - vb,
               grp * G::HD + hi - vb, max(lo, vb) - lo);
     };
-    auto stage_qkv = [&](int layer) {
-        if constexpr (LONG)
-            stage_qkv_all(layer);
-        else
-            stage_qkv_group(layer);
-    };
+    auto stage_qkv = [&](int layer) { stage_qkv_group(layer); };
     auto stage_wo = [&](int layer) {
         if constexpr (LONG) {
             stage(r2, G::ROWS_WO, G::RB_DIM, G::SB_DIM, layer, 3, wo_b, wo_e, 0);
@@ -428,11 +414,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         sc = reinterpret_cast<const uint16_t *>(region + rows * rb + s * sb);
     };
 
-    // Fused attention: each layer's exchanges in write-once words of their
-    // own (q/k/v, h after Wo, act, h after W2); split attention keeps the
-    // tagged words.
-    // (q/k/v by group: group g's GR rows at g GR; the Wo partial sums of
-    // group g at ON_WO + g DIM)
+    // Each layer's exchanges in write-once words of their own: q/k/v by
+    // group (group g's GR rows at g GR), then with the fused attention the
+    // Wo partial sums of group g at ON_WO + g DIM, with split attention the
+    // merged context at ON_WO and h after Wo at ON_WO + DIM; act at ON_GU,
+    // h after W2 at ON_DN. Split attention's partials stay tagged words.
     constexpr int ON_WO = G::DIM + 2 * G::KVD, ON_GU = ON_WO + G::KVH * G::DIM;
     constexpr int ON_DN = ON_GU + G::FFN;
     constexpr int ONCE = ON_DN + G::DIM;
@@ -441,9 +427,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     };
 
     int count = 0, done = 0, last_token = 0;
-    // Tag of the hidden state the next classifier reads; 0 = hidden_in.
-    unsigned hidden_tag = 0;
-    // The same hidden state's write-once words (fused attention).
+    // Write-once words of the hidden state the next classifier reads; null
+    // = hidden_in.
     const float *hidden_once = nullptr;
     // Each phase's weight rows (and attention's K/V rows) are issued just
     // before the wait for its input. Measured: issuing them a phase earlier
@@ -459,13 +444,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             Slice<G::DIM> nw;
             nw.load(a.final_norm);
             float sq;
-            if (hidden_tag == 0) {
+            if (hidden_once == nullptr) {
                 Slice<G::DIM> h;
                 h.load(a.hidden_in);
                 sq = h.store(h_raw);
                 __syncthreads();
-            } else if constexpr (LONG) {
-                sq = take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
             } else {
                 sq = take_once<G::DIM, false>(hidden_once, h_raw, error);
             }
@@ -522,23 +505,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // RoPE factors of this wave's first pair, read before the wait.
             // Pair `pair` of this workgroup: its first row's index in the
             // exchange, which matrix (q, k, v), its dim d and its KV head.
-            const int npairs = LONG ? qkv_e - qkv_b : G::GR_WG / 2;
+            const int npairs = G::GR_WG / 2;
             auto qkv_row = [&](int pair, int &xrow, int &which, int &d, int &kvh) {
-                if constexpr (LONG) {
-                    const int row = 2 * (qkv_b + pair);
-                    which = row < G::DIM ? 0 : row < G::DIM + G::KVD ? 1 : 2;
-                    const int local = which == 0 ? row : which == 1 ? row - G::DIM
-                                                                    : row - G::DIM - G::KVD;
-                    kvh = local / G::HD;
-                    d = local % G::HD;
-                    xrow = row;
-                } else {
-                    const int lr = gj * G::GR_WG + 2 * pair;
-                    which = lr < G::GQ ? 0 : lr < G::GQ + G::HD ? 1 : 2;
-                    d = lr % G::HD;
-                    kvh = grp;
-                    xrow = grp * G::GR + lr;
-                }
+                const int lr = gj * G::GR_WG + 2 * pair;
+                which = lr < G::GQ ? 0 : lr < G::GQ + G::HD ? 1 : 2;
+                d = lr % G::HD;
+                kvh = grp;
+                xrow = grp * G::GR + lr;
             };
             float2 rope_cs = make_float2(1.0f, 0.0f);
             if (wave < npairs) {
@@ -555,8 +528,6 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 e.load(a.embeddings + size_t(token) * G::DIM);
                 sq = e.store(h_raw);
                 dma_wait();
-            } else if constexpr (LONG) {
-                sq = take<G::DIM, false, false, PollDelay<LONG>::A>(a.x_hidden, h_raw, tag - 1, error);
             } else {
                 sq = take_once<G::DIM, false, PollDelay<LONG>::A>(once(it, l - 1, ON_DN), h_raw,
                                                                    error);
@@ -583,13 +554,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                             e0 = fmaf(even, cs.x, -(odd * cs.y));
                             e1 = fmaf(even, cs.y, odd * cs.x);
                         }
-                        if constexpr (LONG) {
-                            put(a.x_qkv + row, e0, tag);
-                            put(a.x_qkv + row + 1, e1, tag);
-                        } else {
-                            put_once(once(it, l, 0) + row, e0);
-                            put_once(once(it, l, 0) + row + 1, e1);
-                        }
+                        put_once(once(it, l, 0) + row, e0);
+                        put_once(once(it, l, 0) + row + 1, e1);
                         if (which > 0) {
                             float *cache = (which == 1 ? kc : vc) +
                                            (size_t(head) * a.max_seq + pos) * G::HD + d;
@@ -630,19 +596,14 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
-            if constexpr (LONG)
-                take<G::DIM + 2 * G::KVD, false, false, PollDelay<LONG>::B>(a.x_qkv, qkv, tag - 1,
-                                                                            error);
-            else
-                take_once<G::GR, false, PollDelay<LONG>::B>(once(it, l, 0) + grp * G::GR, qkv,
-                                                            error);
+            take_once<G::GR, false, PollDelay<LONG>::B>(once(it, l, 0) + grp * G::GR, qkv, error);
             if (LONG) {
                 // the new position's K/V row, when it falls in this unit
                 if (pos >= ap0 && pos < ap1)
                     for (int i = threadIdx.x; i < 2 * G::HD; i += kThreads) {
                         const int which = i >= G::HD, d = i - which * G::HD;
                         (which ? vst : kst)[(pos - ap0) * G::KROW + d] =
-                            qkv[G::DIM + which * G::KVD + ag * G::HD + d];
+                            qkv[G::GQ + which * G::HD + d];
                     }
             } else {
                 // qkv holds the group's q rows, then its k and v rows
@@ -655,10 +616,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             __syncthreads();
             mark(it, 5 + 13 * l);
             if constexpr (LONG) {
-                split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, tag, error);
-                tag += 2;
+                split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, once(it, l, ON_WO),
+                                   tag, error);
+                tag++;
                 // the whole context, as digits for the Wo rows
-                take<G::DIM, false, false, PollDelay<true>::CONTEXT>(a.x_ctx, qkv, tag - 1, error);
+                take_once<G::DIM, false, PollDelay<true>::CONTEXT>(once(it, l, ON_WO), qkv, error);
                 quartet_digits<G::QT>(reinterpret_cast<const float4 *>(qkv)[threadIdx.x],
                                       threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             } else {
@@ -719,7 +681,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
                     const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xl, xsc, G::BLK_DIM);
                     if (lane == 0)
-                        put(a.x_hidden + wo_b + r, h_raw[wo_b + r] + y, tag);
+                        put_once(once(it, l, ON_WO) + G::DIM + wo_b + r, h_raw[wo_b + r] + y);
                 }
             } else {
                 // Wo partial sums over the group's context columns: wave w
@@ -748,8 +710,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
             if constexpr (LONG)
-                sq = take<G::DIM, false, false, PollDelay<LONG>::C>(a.x_hidden, h_raw, tag - 1,
-                                                                    error);
+                sq = take_once<G::DIM, false, PollDelay<LONG>::C>(once(it, l, ON_WO) + G::DIM,
+                                                                  h_raw, error);
             else
                 sq = take_once_sum<G::DIM, G::KVH, PollDelay<LONG>::C>(once(it, l, ON_WO), h_raw,
                                                                       error);
@@ -766,11 +728,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const float g = row_dot<G::QT>(dg, sg, x, G::BLK_DIM);
                     const float u = row_dot<G::QT>(du, su, x, G::BLK_DIM);
                     if (lane == 0) {
-                        const float act = g / (1.0f + expf(-g)) * u;
-                        if constexpr (LONG)
-                            put(a.x_act + gu_b + pair, act, tag);
-                        else
-                            put_once(once(it, l, ON_GU) + gu_b + pair, act);
+                        put_once(once(it, l, ON_GU) + gu_b + pair, g / (1.0f + expf(-g)) * u);
                     }
                 }
             }
@@ -781,10 +739,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
-            if constexpr (LONG)
-                take<G::FFN, true, false, PollDelay<LONG>::D>(a.x_act, xs, tag - 1, error);
-            else
-                take_once<G::FFN, true, PollDelay<LONG>::D>(once(it, l, ON_GU), xs, error);
+            take_once<G::FFN, true, PollDelay<LONG>::D>(once(it, l, ON_GU), xs, error);
             block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {
@@ -796,10 +751,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const float y = row_dot_floats<G::QT, G::CPL_FFN>(d, s, xs, xsc, G::BLK_FFN);
                     if (lane == 0) {
                         const float v = h_raw[dn_b + r] + y;
-                        if constexpr (LONG)
-                            put(a.x_hidden + dn_b + r, v, tag);
-                        else
-                            put_once(once(it, l, ON_DN) + dn_b + r, v);
+                        put_once(once(it, l, ON_DN) + dn_b + r, v);
                         if (last && it + 1 == a.n_iter)
                             a.hidden_out[dn_b + r] = v;
                     }
@@ -809,9 +761,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 if (!last)
                     stage_qkv(l + 1);
             }
-            hidden_tag = tag;
-            if constexpr (!LONG)
-                hidden_once = once(it, l, ON_DN);
+            hidden_once = once(it, l, ON_DN);
             tag++;
             mark(it, 14 + 13 * l);
         }
@@ -819,11 +769,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             break;
     }
     // hidden_out after an early stop (eos): the state the loop ended with
-    if (done && hidden_tag != 0) {
-        if constexpr (LONG)
-            take<G::DIM, false>(a.x_hidden, h_raw, hidden_tag, error);
-        else
-            take_once<G::DIM, false>(hidden_once, h_raw, error);
+    if (done && hidden_once != nullptr) {
+        take_once<G::DIM, false>(hidden_once, h_raw, error);
         for (int i = threadIdx.x; i < G::DIM; i += kThreads)
             if (blockIdx.x == 0)
                 a.hidden_out[i] = h_raw[i];
@@ -876,10 +823,10 @@ void launch_as(const TokenArgs &args, hipStream_t stream)
             "token kernel: context exceeds the attention pass");
     require(token_tags_needed(args.n_iter, args.layer_count) <= (1ll << kTagShift), NUT_EINVAL,
             "token kernel: launch exceeds its exchange tag range");
-    require(!LONG || (args.x_apart != nullptr && args.x_ctx != nullptr), NUT_EINVAL,
+    require(!LONG || args.x_apart != nullptr, NUT_EINVAL,
             "token kernel: split attention needs its exchange buffers");
-    require(LONG || args.x_once != nullptr, NUT_EINVAL,
-            "token kernel: fused attention needs its write-once exchange words");
+    require(args.x_once != nullptr, NUT_EINVAL,
+            "token kernel: the launch needs its write-once exchange words");
     static_assert(Lds<G>::BYTES > 0 && G::DIM % 2 == 0 && G::KVD % 2 == 0 && G::FFN % 2 == 0,
                   "write-once words are polled in pairs");
     TokenArgs a = args;

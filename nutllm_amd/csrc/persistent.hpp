@@ -27,10 +27,9 @@ struct TokenArgs {
     const float2 *rope;
     float *k_cache, *v_cache; // [layer][kv_head][max_seq][head_dim]
     uint64_t *x_qkv, *x_hidden, *x_act, *x_part; // tagged exchange buffers
-    // Fused attention (long_attention == 0) and the wide kernel: the h, act
-    // and (q/k/v or context) exchanges in write-once words
-    // (token_once_floats of them, every word kUnset = 0xffffffff when the
-    // launch starts), iteration it and layer l at
+    // The q/k/v (or the wide kernel's context), h and act exchanges in
+    // write-once words (token_once_floats of them, every word kUnset =
+    // 0xffffffff when the launch starts), iteration it and layer l at
     // x_once + (it * layer_count + l) * token_once_stride.
     float *x_once;
     // Long contexts (long_attention != 0): attention is split over the
@@ -63,8 +62,9 @@ struct TokenArgs {
 // classifier8); larger vocabularies take the plain fp32 pass.
 constexpr int kScreenRowsMax = 1024;
 
-// Write-once words per iteration and layer. The fused-attention kernel:
-// q/k/v, the Wo partial sums of each KV head group (h after Wo), act, h
+// Write-once words per iteration and layer. The TinyLlama-shape kernel:
+// q/k/v, the Wo partial sums of each KV head group (fused attention; split
+// attention puts the merged context and h after Wo in that space), act, h
 // after W2. The wide kernel (wide.hip): the context, h after Wo, act, h
 // after W2.
 inline size_t token_once_stride(const DecodeShape &s, bool wide)
