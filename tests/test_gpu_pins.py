@@ -83,6 +83,38 @@ def test_nonunit_norms_token_kernel_fused(gpu, qtype):
         dev.close()
 
 
+@pytest.mark.parametrize("qtype", [0, 1], ids=["int8", "int4"])
+def test_token_kernel_fused_attention_past_32_positions(gpu, qtype):
+    """The fused attention near the end of its pass (48 positions INT4, 44
+    INT8): a 30-token prompt through the kernel's prefill loop, decode steps
+    at positions 30..43 (hidden state and every layer's new K/V rows), then
+    12 greedy ids from position 30, against the oracle with non-unit norm
+    weights."""
+    O.orc().orc_set_threads(16)
+    model = W.build("tinyllama", qtype, 3, 64, norm_seed=NORM_SEED)
+    c = model.config
+    prompt = gpu.synth_tokens(5, c.vocab_size, 30)
+    dev = model.to_device()
+    om = O.oracle_model(model)
+    try:
+        dev.set_path(2)
+        cache = gpu.KVCache(c)
+        assert rel_l2(dev.prefill(cache, prompt), om.prefill(prompt)) <= TOL
+        for step in range(14):
+            token = 7 + 991 * step
+            err = rel_l2(dev.decode(cache, token), om.decode(token))
+            print(f"qtype {qtype} position {len(prompt) + step}: hidden rel-L2 {err:.2e}",
+                  flush=True)
+            assert err <= TOL
+            check_kv(cache, om, c, [len(prompt) + step])
+        ids, _ = dev.generate(prompt, 12)
+        ref, _, _ = om.generate(prompt, 12)
+        assert ids == ref
+    finally:
+        dev.set_path(0)
+        dev.close()
+
+
 def test_nonunit_norms_token_kernel_split(gpu):
     """Token kernel past its fused pass (split attention over the grid):
     from a 120-token step-kernel prefill, three token-kernel decode steps
