@@ -96,11 +96,11 @@ def cpu_info():
     return model, n
 
 
-def counter_pass(counter):
-    """One rocprofv3 counter pass over a single generate of this workload
-    (a child process: python3 bench.py under rocprofv3 --pmc COUNTER), plus
-    a CALIBRATE_MIB device-to-device copy in the same process. Returns
-    (KiB per token-kernel dispatch, KiB per copy dispatch)."""
+def counter_pass(counter, workload):
+    """One rocprofv3 counter pass over a single generate of `workload` (a
+    child process: python3 bench.py under rocprofv3 --pmc COUNTER), plus a
+    CALIBRATE_MIB device-to-device copy in the same process. Returns
+    (KiB per decode-kernel dispatch, KiB per copy dispatch)."""
     import glob
     import shutil
     import signal
@@ -111,7 +111,8 @@ def counter_pass(counter):
     out = tempfile.mkdtemp(prefix="nut_pmc_")
     cmd = [tool, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--",
            sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-traffic",
-           "--steps", "1", "--warmup", "0", "--calibrate-copy-mib", str(CALIBRATE_MIB)]
+           "--workload", workload, "--steps", "1", "--warmup", "0",
+           "--calibrate-copy-mib", str(CALIBRATE_MIB)]
     proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
                             start_new_session=True)
     try:
@@ -131,9 +132,11 @@ def counter_pass(counter):
 
 
 def parse_counter_csv(files, counter):
-    """(mean value per token-kernel dispatch, value of the largest copy
-    dispatch) of `counter` in rocprofv3 counter-collection CSV files. A
-    dispatch's rows (one per counter in the files seen here) are summed."""
+    """(mean value per decode-kernel dispatch, value of the largest copy
+    dispatch) of `counter` in rocprofv3 counter-collection CSV files. The
+    decode kernels are the cooperative generate launches (token_kernel, and
+    wide_kernel at the 7B widths); a dispatch's rows (one per counter in the
+    files seen here) are summed."""
     import csv
     kernel, copy = {}, {}
     for name in files:
@@ -144,25 +147,27 @@ def parse_counter_csv(files, counter):
                 key = (name, row.get("Dispatch_Id", ""))
                 v = float(row["Counter_Value"])
                 k = row.get("Kernel_Name", "")
-                if "token_kernel" in k:
+                if "token_kernel" in k or "wide_kernel" in k:
                     kernel[key] = kernel.get(key, 0.0) + v
                 elif "copyBuffer" in k:
                     copy[key] = copy.get(key, 0.0) + v
     if not kernel or not copy:
-        raise RuntimeError(f"{counter} pass: no token-kernel or copy dispatch")
+        raise RuntimeError(f"{counter} pass: no decode-kernel or copy dispatch")
     # the calibration copies are the largest copy dispatches (model upload
     # copies are small)
     return statistics.mean(kernel.values()), max(copy.values())
 
 
-def measured_traffic():
-    """HBM bytes of one generate launch (16 iterations) from FETCH_SIZE and
+def measured_traffic(workload):
+    """HBM bytes of one generate launch of `workload` from FETCH_SIZE and
     WRITE_SIZE counter passes of this build, each scaled by what the counter
     reads for the CALIBRATE_MIB copy: FETCH_SIZE counts half of a copy's read
     bytes on this GPU, WRITE_SIZE all of its written bytes."""
     true_kib = CALIBRATE_MIB * 1024
-    fetch, fetch_copy = counter_pass("FETCH_SIZE")
-    write, write_copy = counter_pass("WRITE_SIZE")
+    fetch, fetch_copy = counter_pass("FETCH_SIZE", workload)
+    log("FETCH_SIZE pass done")
+    write, write_copy = counter_pass("WRITE_SIZE", workload)
+    log("WRITE_SIZE pass done")
     f_scale, w_scale = true_kib / fetch_copy, true_kib / write_copy
     return {"bytes": int(round((fetch * f_scale + write * w_scale) * 1024)),
             "fetch_kib": round(fetch, 1), "fetch_scale": round(f_scale, 5),
@@ -225,7 +230,31 @@ def cpu_baseline(model, prompt, gen):
     }, ids
 
 
-def long_prompt(args, nut, workloads):
+def calibration_copy(args, nut):
+    """The known-size copy that scales a counter pass's FETCH_SIZE and
+    WRITE_SIZE (--calibrate-copy-mib; nothing when 0)."""
+    if args.calibrate_copy_mib > 0:
+        nbytes = args.calibrate_copy_mib << 20
+        src, dst = nut.DeviceArray(nbytes), nut.DeviceArray(nbytes)
+        for _ in range(2):
+            nut.check(nut.lib().nut_memcpy_d2d(dst.ptr, src.ptr, nbytes))
+        src.close(), dst.close()
+        log(f"copied {args.calibrate_copy_mib} MiB device to device, twice")
+
+
+def add_traffic(line, traffic, traffic_error):
+    """roofline.traffic (HBM bytes per generate launch, measured) and its
+    ratio to the algorithmic bytes, or the reason it was not measured."""
+    roof = line["roofline"]
+    if traffic is not None:
+        roof["traffic"] = traffic["bytes"]
+        roof["traffic_ratio"] = round(traffic["bytes"] / roof["bytes_per_launch"], 4)
+        roof["traffic_counters"] = traffic
+    elif traffic_error is not None:
+        roof["traffic_error"] = traffic_error
+
+
+def long_prompt(args, nut, workloads, traffic=None, traffic_error=None):
     """Prefill (batched GEMM path) and decode of a long-prompt run."""
     import numpy as np
     t = time.time()
@@ -314,6 +343,8 @@ def long_prompt(args, nut, workloads):
                              "flop": flop},
         "ids_match_reference": None if ref_ids is None else ids == ref_ids,
     }
+    add_traffic(line, traffic, traffic_error)
+    calibration_copy(args, nut)
     if not args.no_cpu:
         line["cpu_baseline"] = long_cpu_baseline(model, prompt, ids)
     print(json.dumps(line), flush=True)
@@ -432,12 +463,13 @@ def main():
         sys.exit(2)
 
     # The counter passes run as child processes before this process touches
-    # the GPU (default workload only).
+    # the GPU (decode workloads on the cooperative generate kernels).
     traffic, traffic_error = None, None
-    if args.workload == "tinyllama_int4" and not args.no_traffic:
+    if (args.workload != "kernels" and not args.prefill_only and args.path != "steps"
+            and not args.no_traffic):
         log("measuring HBM traffic (two rocprofv3 counter passes)")
         try:
-            traffic = measured_traffic()
+            traffic = measured_traffic(args.workload)
         except (RuntimeError, OSError, ValueError, KeyError) as e:
             traffic_error = str(e)
             log(f"traffic not measured: {e}")
@@ -452,7 +484,7 @@ def main():
         kernels(args)
         return
     if args.workload != "tinyllama_int4":
-        long_prompt(args, nut, workloads)
+        long_prompt(args, nut, workloads, traffic, traffic_error)
         return
     t = time.time()
     model, prompt, gen = workloads.build_run("tinyllama_int4")
@@ -531,13 +563,7 @@ def main():
         line["roofline"]["traffic_counters"] = traffic
     elif traffic_error is not None:
         line["roofline"]["traffic_error"] = traffic_error
-    if args.calibrate_copy_mib > 0:
-        nbytes = args.calibrate_copy_mib << 20
-        src, dst = nut.DeviceArray(nbytes), nut.DeviceArray(nbytes)
-        for _ in range(2):
-            nut.check(nut.lib().nut_memcpy_d2d(dst.ptr, src.ptr, nbytes))
-        src.close(), dst.close()
-        log(f"copied {args.calibrate_copy_mib} MiB device to device, twice")
+    calibration_copy(args, nut)
     if not args.no_cpu:
         log("timing the CPU baseline")
         base, cpu_ids = cpu_baseline(model, prompt, gen)

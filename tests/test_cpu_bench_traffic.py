@@ -48,3 +48,31 @@ def test_parse_counter_csv_missing(tmp_path):
     f.write_text(HEADER + "\n" + row(1, "qkv_fast_kernel<1, 2>", "FETCH_SIZE", 1.0) + "\n")
     with pytest.raises(RuntimeError):
         b.parse_counter_csv([str(f)], "FETCH_SIZE")
+
+
+def test_parse_counter_csv_wide_kernel(tmp_path):
+    """The 7B-width decode runs on wide_kernel: its dispatches count as the
+    decode launches, prefill kernels do not."""
+    b = bench()
+    k = "void nut::(anonymous namespace)::wide_kernel<WideGeo<1>, true>(nut::TokenArgs)"
+    lines = [HEADER,
+             row(1, "prefill_gemm_kernel<1>", "WRITE_SIZE", 900.0),
+             row(2, k, "WRITE_SIZE", 30.0), row(2, k, "WRITE_SIZE", 2.0),
+             row(3, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 1048576.0)]
+    f = tmp_path / "run_counter_collection.csv"
+    f.write_text("\n".join(lines) + "\n")
+    kernel, copy = b.parse_counter_csv([str(f)], "WRITE_SIZE")
+    assert kernel == pytest.approx(32.0)
+    assert copy == pytest.approx(1048576.0)
+
+
+def test_add_traffic_ratio():
+    b = bench()
+    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None}}
+    b.add_traffic(line, {"bytes": 1085, "fetch_kib": 1.0}, None)
+    assert line["roofline"]["traffic"] == 1085
+    assert line["roofline"]["traffic_ratio"] == pytest.approx(1.085)
+    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None}}
+    b.add_traffic(line, None, "FETCH_SIZE pass timed out")
+    assert line["roofline"]["traffic"] is None
+    assert line["roofline"]["traffic_error"] == "FETCH_SIZE pass timed out"
