@@ -579,16 +579,19 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             const int ap1 = min(n, ap0 + per);
             // fused: the group's KV head only, K rows [n][KROW] then V rows
             float *vst = LONG ? kst + G::PMAX * G::KROW : kst + n * G::KROW;
+            // Rows before pos only: they were stored by earlier launches or
+            // by other workgroups in earlier iterations of this one, hence
+            // the agent-coherent loads; row pos comes from the exchange.
             if (LONG) {
                 const int hist = max(0, min(ap1, pos) - ap0); // rows already cached
                 if (hist > 0) {
                     const size_t row0 = size_t(ag) * a.max_seq + ap0;
-                    dma_padded_rows<kStreamPolicy>(kst, kc + row0 * G::HD, hist);
-                    dma_padded_rows<kStreamPolicy>(vst, vc + row0 * G::HD, hist);
+                    dma_padded_rows<kStreamPolicy | kAgentCoherent>(kst, kc + row0 * G::HD, hist);
+                    dma_padded_rows<kStreamPolicy | kAgentCoherent>(vst, vc + row0 * G::HD, hist);
                 }
             } else if (pos > 0) {
-                dma_padded_rows(kst, kc + size_t(grp) * a.max_seq * G::HD, pos);
-                dma_padded_rows(vst, vc + size_t(grp) * a.max_seq * G::HD, pos);
+                dma_padded_rows<kAgentCoherent>(kst, kc + size_t(grp) * a.max_seq * G::HD, pos);
+                dma_padded_rows<kAgentCoherent>(vst, vc + size_t(grp) * a.max_seq * G::HD, pos);
             }
             stage_wo(l);
             mark(it, 4 + 13 * l);

@@ -142,12 +142,25 @@ __device__ __forceinline__ void dma_wait()
     __syncthreads();
 }
 
+// sc1 (bit 4 of the cache-policy field): the load is coherent at agent
+// scope, as the relaxed agent-scope atomic loads of the exchange are
+// (gfx950 compiles those to `global_load ... sc1`). K/V cache rows that
+// another workgroup stored earlier in the same launch are staged with it:
+// those rows were written with agent-scope stores (sc1) from CUs on other
+// XCDs, and a load without sc1 may be served by a line that its own XCD's
+// L2 or its CU's L1 held before the write. The stores are retired by the
+// writer's s_waitcnt vmcnt(0) before its next publish, and the reader issues
+// the staging only after it has seen a later publish of that writer, so an
+// agent-coherent load returns the stored row.
+constexpr int kAgentCoherent = 16;
+
 // Rows [0, n) of 64-float rows at src into LDS rows of 68 floats (16 data
 // granules + 1 spare): LDS granule j holds row j / 17, granule j % 17.
-// POLICY is the loads' cache policy: 0 where every workgroup stages the
-// same rows (they stay in L2), kStreamPolicy where each row is staged by one
-// workgroup once per token.
-template <int POLICY = 0>
+// POLICY is the loads' cache policy, which for K/V cache rows includes
+// kAgentCoherent: alone where every workgroup of a KV head group stages the
+// same rows, with kStreamPolicy where each row is staged by one workgroup
+// once per token.
+template <int POLICY>
 __device__ __forceinline__ void dma_padded_rows(float *lds_dst,
                                                 const float *src, int n)
 {
