@@ -9,20 +9,21 @@ resident in HBM before the timed region.
 
 value     decode tok/s with the reference's GenerationStats semantics
           (every classifier + argmax + decode step after the prefill).
-roofline  algorithmic bytes of the decode loop (packed weights + fp16 scales
-          + the classifier's INT8 block-32 screening copy + norms + one
-          embedding row per token, plus K/V reads) / device time of the
-          decode loop from HIP events on the model's stream, against the
-          8 TB/s HBM peak. The argmax reads the fp32 classifier rows only
-          for the few rows the copy's error bounds cannot rule out (not
-          counted).
-model_weight_roofline  the same with the model's own weight bytes (the
-          fp32 classifier as stored): weight bytes per token / step time.
+roofline  algorithmic bytes of the decode loop (the model's weight bytes per
+          token: packed weights + fp16 scales of every projection, the fp32
+          classifier as stored, norms, one embedding row; plus K/V reads) /
+          device time of the decode loop from HIP events on the model's
+          stream, against the 8 TB/s HBM peak.
           roofline.traffic: HBM bytes per generate launch measured in the same
           run, before the timed region, by two rocprofv3 counter passes
           (FETCH_SIZE, WRITE_SIZE) over a child run of this script, each
           scaled by the counter's reading for a 1 GiB device-to-device copy
-          (--no-traffic skips them; traffic is then null).
+          (--no-traffic skips them; traffic is then null); each pass's exit
+          status is kept in traffic_counters.
+screened_roofline  the same over the bytes the decode loop actually reads:
+          the greedy argmax goes through the classifier's INT8 block-32
+          screening copy and recomputes fp32 logits only for the few rows
+          its error bounds cannot rule out (those rows not counted).
 cpu_baseline  the compiled reference's own threaded generate_tokens_cached
           (oracle/_ref, "reference") or, when that library is absent, this
           repo's C restatement ("port"), timed on this host in the same run
@@ -100,7 +101,8 @@ def counter_pass(counter, workload):
     """One rocprofv3 counter pass over a single generate of `workload` (a
     child process: python3 bench.py under rocprofv3 --pmc COUNTER), plus a
     CALIBRATE_MIB device-to-device copy in the same process. Returns
-    (KiB per decode-kernel dispatch, KiB per copy dispatch)."""
+    (KiB per decode-kernel dispatch, KiB per copy dispatch, the child's exit
+    status: negative for a signal)."""
     import glob
     import shutil
     import signal
@@ -121,10 +123,12 @@ def counter_pass(counter, workload):
         os.killpg(proc.pid, signal.SIGKILL)
         proc.wait()
         raise RuntimeError(f"{counter} pass timed out")
-    # (the tool can end with SIGSEGV in exit() after writing complete files)
+    # The tool can end with SIGSEGV in exit() after writing complete files;
+    # the status is returned with the counts so the line records it.
     files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
     try:
-        return parse_counter_csv(files, counter)
+        kernel, copy = parse_counter_csv(files, counter)
+        return kernel, copy, proc.returncode
     except RuntimeError as e:
         raise RuntimeError(f"{e} (exit status {proc.returncode})") from None
     finally:
@@ -164,14 +168,15 @@ def measured_traffic(workload):
     reads for the CALIBRATE_MIB copy: FETCH_SIZE counts half of a copy's read
     bytes on this GPU, WRITE_SIZE all of its written bytes."""
     true_kib = CALIBRATE_MIB * 1024
-    fetch, fetch_copy = counter_pass("FETCH_SIZE", workload)
-    log("FETCH_SIZE pass done")
-    write, write_copy = counter_pass("WRITE_SIZE", workload)
-    log("WRITE_SIZE pass done")
+    fetch, fetch_copy, fetch_rc = counter_pass("FETCH_SIZE", workload)
+    log(f"FETCH_SIZE pass done (exit status {fetch_rc})")
+    write, write_copy, write_rc = counter_pass("WRITE_SIZE", workload)
+    log(f"WRITE_SIZE pass done (exit status {write_rc})")
     f_scale, w_scale = true_kib / fetch_copy, true_kib / write_copy
     return {"bytes": int(round((fetch * f_scale + write * w_scale) * 1024)),
             "fetch_kib": round(fetch, 1), "fetch_scale": round(f_scale, 5),
-            "write_kib": round(write, 1), "write_scale": round(w_scale, 5)}
+            "write_kib": round(write, 1), "write_scale": round(w_scale, 5),
+            "fetch_exit_status": fetch_rc, "write_exit_status": write_rc}
 
 
 def kv_bytes_per_position(cfg):
@@ -243,15 +248,32 @@ def calibration_copy(args, nut):
 
 
 def add_traffic(line, traffic, traffic_error):
-    """roofline.traffic (HBM bytes per generate launch, measured) and its
-    ratio to the algorithmic bytes, or the reason it was not measured."""
+    """roofline.traffic (HBM bytes per generate launch, measured), its ratio
+    to the algorithmic bytes and to the bytes the loop reads (screened
+    classifier), or the reason it was not measured."""
     roof = line["roofline"]
     if traffic is not None:
         roof["traffic"] = traffic["bytes"]
         roof["traffic_ratio"] = round(traffic["bytes"] / roof["bytes_per_launch"], 4)
+        roof["traffic_ratio_bytes_read"] = round(
+            traffic["bytes"] / line["screened_roofline"]["bytes_per_launch"], 4)
         roof["traffic_counters"] = traffic
     elif traffic_error is not None:
         roof["traffic_error"] = traffic_error
+
+
+def decode_rooflines(model_bytes, read_bytes, device_ms, kernel):
+    """roofline (the model's weight bytes + K/V per launch over the decode
+    loop's device time) and screened_roofline (the bytes the loop reads)."""
+    achieved = model_bytes / (device_ms * 1e-3) / 1e9
+    read = read_bytes / (device_ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": kernel, "bytes_per_launch": model_bytes,
+            "device_ms_per_launch": round(device_ms, 4)}
+    screened = {"achieved": round(read, 1), "unit": "GB/s",
+                "frac": round(read / HBM_PEAK_GBS, 4), "bytes_per_launch": read_bytes}
+    return roof, screened
 
 
 def long_prompt(args, nut, workloads, traffic=None, traffic_error=None):
@@ -309,10 +331,11 @@ def long_prompt(args, nut, workloads, traffic=None, traffic_error=None):
     per_pos = kv_bytes_per_position(cfg)
     kv_bytes = sum(per_pos * (len(prompt) + i + 1) for i in range(n))
     screened = args.path != "steps"  # the token kernels screen the classifier
-    step_bytes = model.weight_bytes_per_token(screened=screened) * n + kv_bytes
+    read_bytes = model.weight_bytes_per_token(screened=screened) * n + kv_bytes
     model_bytes = model.weight_bytes_per_token() * n + kv_bytes
-    achieved = step_bytes / (device_ms * 1e-3) / 1e9
-    model_achieved = model_bytes / (device_ms * 1e-3) / 1e9
+    roof, screened_roof = decode_rooflines(
+        model_bytes, read_bytes, device_ms,
+        "decode loop (classifier + argmax + decode step per token)")
     line = {
         "metric": f"decode tok/s, {args.workload} (greedy, {len(prompt)}-token prompt, "
                   f"{gen} tokens)",
@@ -328,13 +351,8 @@ def long_prompt(args, nut, workloads, traffic=None, traffic_error=None):
                    "ffn_dim": cfg.ffn_dim, "vocab": cfg.vocab_size,
                    "prompt_tokens": len(prompt), "generated_tokens": n},
         "decode_device_us_per_token": round(device_ms * 1e3 / n, 1),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "decode loop (classifier + argmax + "
-                     "decode step per token)", "bytes_per_launch": step_bytes},
-        "model_weight_roofline": {"achieved": round(model_achieved, 1), "unit": "GB/s",
-                                  "frac": round(model_achieved / HBM_PEAK_GBS, 4),
-                                  "bytes_per_launch": model_bytes},
+        "roofline": roof,
+        "screened_roofline": screened_roof,
         "prefill_tok_s": round(len(prompt) / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 2),
         "prefill_roofline": {"bound": "mfma", "achieved": round(flop / prefill_s / 1e12, 1),
@@ -513,10 +531,11 @@ def main():
     per_pos = kv_bytes_per_position(cfg)
     # each decode-loop iteration at cache length P+i reads K/V of P+i+1
     kv_bytes = sum(per_pos * (len(prompt) + i + 1) for i in range(n))
-    step_bytes = model.weight_bytes_per_token(screened=True) * n + kv_bytes
+    read_bytes = model.weight_bytes_per_token(screened=True) * n + kv_bytes
     model_bytes = model.weight_bytes_per_token() * n + kv_bytes
-    achieved = step_bytes / (statistics.median(device_ms) * 1e-3) / 1e9
-    model_achieved = model_bytes / (statistics.median(device_ms) * 1e-3) / 1e9
+    roof, screened_roof = decode_rooflines(
+        model_bytes, read_bytes, statistics.median(device_ms),
+        "decode loop (classifier + argmax + decode step per token)")
     line = {
         "metric": "decode tok/s, TinyLlama-1.1B-shape INT4 (greedy, 5-token "
                   "prompt, 16 tokens)",
@@ -541,28 +560,10 @@ def main():
         "prefill_tok_s": round(len(prompt) / statistics.median(prefill_s), 3),
         "decode_device_us_per_token": round(
             statistics.median(device_ms) * 1e3 / n, 2),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None if traffic is None else traffic["bytes"],
-            "kernel": "decode loop (classifier + argmax + decode step per "
-                      "token)",
-            "bytes_per_launch": step_bytes,
-        },
-        "model_weight_roofline": {
-            "achieved": round(model_achieved, 1), "unit": "GB/s",
-            "frac": round(model_achieved / HBM_PEAK_GBS, 4),
-            "bytes_per_launch": model_bytes,
-        },
+        "roofline": roof,
+        "screened_roofline": screened_roof,
     }
-    if traffic is not None:
-        line["roofline"]["traffic_ratio"] = round(traffic["bytes"] / step_bytes, 4)
-        line["roofline"]["traffic_counters"] = traffic
-    elif traffic_error is not None:
-        line["roofline"]["traffic_error"] = traffic_error
+    add_traffic(line, traffic, traffic_error)
     calibration_copy(args, nut)
     if not args.no_cpu:
         log("timing the CPU baseline")

@@ -68,11 +68,33 @@ def test_parse_counter_csv_wide_kernel(tmp_path):
 
 def test_add_traffic_ratio():
     b = bench()
-    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None}}
-    b.add_traffic(line, {"bytes": 1085, "fetch_kib": 1.0}, None)
+    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None},
+            "screened_roofline": {"bytes_per_launch": 800}}
+    b.add_traffic(line, {"bytes": 1085, "fetch_kib": 1.0, "fetch_exit_status": -11,
+                         "write_exit_status": 0}, None)
     assert line["roofline"]["traffic"] == 1085
     assert line["roofline"]["traffic_ratio"] == pytest.approx(1.085)
-    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None}}
+    assert line["roofline"]["traffic_ratio_bytes_read"] == pytest.approx(1.3563, abs=1e-4)
+    assert line["roofline"]["traffic_counters"]["fetch_exit_status"] == -11
+    line = {"roofline": {"bytes_per_launch": 1000, "traffic": None},
+            "screened_roofline": {"bytes_per_launch": 800}}
     b.add_traffic(line, None, "FETCH_SIZE pass timed out")
     assert line["roofline"]["traffic"] is None
     assert line["roofline"]["traffic_error"] == "FETCH_SIZE pass timed out"
+
+
+def test_decode_rooflines_use_the_model_weight_bytes():
+    """The line's roofline.frac is the model's weight bytes (fp32 classifier
+    as stored) plus K/V over the decode loop's device time; the bytes the
+    screened argmax reads are the secondary figure. TinyLlama INT4: 807,518,208
+    weight bytes per token."""
+    b = bench()
+    n, kv = 16, 45056 * sum(5 + i + 1 for i in range(16))
+    model_bytes = 807518208 * n + kv
+    read_bytes = 615006208 * n + kv
+    roof, screened = b.decode_rooflines(model_bytes, read_bytes, 5.495275, "k")
+    assert roof["bytes_per_launch"] == 12930023424
+    assert roof["frac"] == pytest.approx(12930023424 / 5.495275e-3 / 8e12, abs=1e-4)
+    assert roof["frac"] == pytest.approx(0.2941, abs=1e-4)
+    assert screened["bytes_per_launch"] == read_bytes
+    assert screened["frac"] < roof["frac"]
