@@ -19,6 +19,9 @@ Files written:
                   the tiny synthetic model quantised by the reference:
                   greedy ids (16), per-step hidden states, final-step
                   logits, KV cache contents
+  tiny_norms_int8.npz, tiny_norms_int4.npz
+                  the same with seeded non-unit attention, ffn and final
+                  norm weights
   tinyllama_int4.json  greedy ids of the TinyLlama-shape INT4 run
                   (5-token prompt, 16 tokens) and its storage_bytes
   fp32_*.npz      the fp32 model path (ModelWeights): prefill_tokens rows
@@ -215,6 +218,33 @@ def write_tiny(qtype, tag):
         storage_bytes=np.int64(storage))
 
 
+NORM_SEED = 9
+
+
+def write_tiny_norms(qtype, tag):
+    """As write_tiny, with seeded non-unit norm weights (attention and ffn
+    norm of both layers, final norm: N(1, 0.25^2), workloads.seeded_norms):
+    the three norms of src/quant_model.cpp:182-190 and
+    src/generate.cpp:197-198 each enter the reference's output."""
+    model = W.build("tiny", qtype, 0, keep_fp32=True, norm_seed=NORM_SEED)
+    c = model.config
+    cfg = {n: getattr(c, n) for n, _ in oracle.OrcConfig._fields_}
+    ref = oracle.RefModel(cfg, qtype, model.embeddings, model.final_norm,
+                          model.lm_head, model.fp32_layers, norms=model.norms)
+    prompt = W.synth_tokens(1, c.vocab_size, 5)
+    ids, _, _ = ref.generate(prompt, 16)
+    tokens = np.concatenate([prompt, np.array(ids[:-1], np.int32)])
+    kv = oracle.orc().orc_kv_elements(oracle.C.byref(oracle.OrcConfig(**cfg)))
+    hidden, keys, values = ref.decode_trace(tokens, kv_elements=kv)
+    logits = ref.logits(hidden[len(prompt) - 1])
+    ref.close()
+    np.savez_compressed(
+        os.path.join(HERE, f"tiny_norms_{tag}.npz"), prompt=prompt,
+        ids=np.array(ids, np.int32), tokens=tokens, hidden=hidden,
+        logits=logits, keys=keys, values=values, norm_seed=np.int64(NORM_SEED),
+        digest=np.array(weight_digest(model)))
+
+
 def write_tinyllama():
     model, prompt, gen = W.build_run("tinyllama_int4")
     c = model.config
@@ -336,6 +366,10 @@ def main():
     if "--only-fp32" in sys.argv:
         write_fp32()
         return
+    if "--only-norms" in sys.argv:
+        write_tiny_norms(INT8, "int8")
+        write_tiny_norms(INT4, "int4")
+        return
     if "--only-long" in sys.argv:
         for name in ("tinyllama_int8_2k", "llama7b_int4"):
             write_long(name)
@@ -344,6 +378,8 @@ def main():
     write_quant_errors()
     write_tiny(INT8, "int8")
     write_tiny(INT4, "int4")
+    write_tiny_norms(INT8, "int8")
+    write_tiny_norms(INT4, "int4")
     copy_fixtures()
     write_fp32()
     if "--skip-tinyllama" not in sys.argv:

@@ -2,7 +2,8 @@
 
 * tiny synthetic model (INT8 and INT4): greedy ids, every decode step's
   hidden state, the final-step logits and the KV cache, bit for bit, against
-  vectors the reference wrote (tests/golden/tiny_*.npz);
+  vectors the reference wrote (tests/golden/tiny_*.npz), with unit norm
+  weights and with seeded non-unit ones (tests/golden/tiny_norms_*.npz);
 * TinyLlama-shape INT4 (5-token prompt, 16 tokens): greedy ids against the
   reference's (tests/golden/tinyllama_int4.json);
 * the reference's llama2.c fixture (tests/fixtures/tiny-llama2.bin, copied
@@ -60,6 +61,47 @@ def test_tiny_model_matches_reference(qtype, tag):
     assert np.array_equal(om.values, g["values"])
     logits = om.logits(g["hidden"][len(g["prompt"]) - 1])
     assert np.array_equal(logits, g["logits"])
+
+
+@pytest.mark.parametrize("qtype,tag", [(INT8, "int8"), (INT4, "int4")])
+def test_tiny_model_with_norms_matches_reference(qtype, tag):
+    """Seeded non-unit attention, ffn and final norms (the three norms of
+    src/quant_model.cpp:182-190 and src/generate.cpp:197-198): the oracle's
+    greedy ids, every decode step's hidden state, the KV cache and the
+    final-step logits equal the reference's bit for bit
+    (tests/golden/tiny_norms_*.npz)."""
+    g = np.load(os.path.join(GOLDEN, f"tiny_norms_{tag}.npz"))
+    model = W.build("tiny", qtype, 0, norm_seed=int(g["norm_seed"]))
+    assert digest(model) == str(g["digest"])
+    om = oracle.oracle_model(model)
+    ids, _, _ = om.generate(g["prompt"], 16)
+    assert ids == g["ids"].tolist()
+    om.reset()
+    for i, token in enumerate(g["tokens"]):
+        h = om.decode(int(token))
+        assert np.array_equal(h, g["hidden"][i]), f"step {i}"
+    assert np.array_equal(om.keys, g["keys"])
+    assert np.array_equal(om.values, g["values"])
+    logits = om.logits(g["hidden"][len(g["prompt"]) - 1])
+    assert np.array_equal(logits, g["logits"])
+
+
+def test_norm_fixtures_tell_the_norms_apart():
+    """The non-unit-norm fixture pins the wiring: with the attention and ffn
+    norms swapped, or the final norm left out, the oracle's output differs
+    from the reference's."""
+    g = np.load(os.path.join(GOLDEN, "tiny_norms_int8.npz"))
+    model = W.build("tiny", INT8, 0, norm_seed=int(g["norm_seed"]))
+    swapped = W.build("tiny", INT8, 0, norm_seed=int(g["norm_seed"]))
+    swapped.norms = [(f, a) for a, f in model.norms]
+    om = oracle.oracle_model(swapped)
+    h = [om.decode(int(t)) for t in g["tokens"][:3]]
+    assert not np.array_equal(h[-1], g["hidden"][2])
+    unit_final = W.build("tiny", INT8, 0, norm_seed=int(g["norm_seed"]))
+    unit_final.final_norm = np.ones_like(model.final_norm)
+    om = oracle.oracle_model(unit_final)
+    logits = om.logits(g["hidden"][len(g["prompt"]) - 1])
+    assert not np.allclose(logits, g["logits"], rtol=1e-3, atol=0)
 
 
 def test_tiny_prefill_equals_decode_loop():

@@ -417,13 +417,15 @@ def test_llama2c_fixture_says_hi(gpu, qtype):
     dev.close()
 
 
+@pytest.mark.parametrize("norms", [False, True], ids=["unit_norms", "seeded_norms"])
 @pytest.mark.parametrize("qtype,tag", [(0, "int8"), (1, "int4")])
-def test_tiny_matches_reference_golden(gpu, qtype, tag):
+def test_tiny_matches_reference_golden(gpu, qtype, tag, norms):
     """Greedy ids equal the reference's; every decode step's hidden state
     and the final-step logits within rel-L2 1e-5 of the reference's
-    (tests/golden/tiny_*.npz)."""
-    g = np.load(os.path.join(GOLDEN, f"tiny_{tag}.npz"))
-    model = W.build("tiny", qtype, 0)
+    (tests/golden/tiny_*.npz; tiny_norms_*.npz with seeded non-unit
+    attention, ffn and final norms)."""
+    g = np.load(os.path.join(GOLDEN, f"tiny_{'norms_' if norms else ''}{tag}.npz"))
+    model = W.build("tiny", qtype, 0, norm_seed=int(g["norm_seed"]) if norms else None)
     dev = model.to_device()
     ids, _ = dev.generate(g["prompt"], 16)
     assert ids == g["ids"].tolist()
