@@ -100,6 +100,10 @@ int nut_device_count(int *count);
 int nut_set_device(int device);
 int nut_malloc(void **d_ptr, size_t bytes);
 int nut_free(void *d_ptr);
+/* Device allocations (hipMalloc calls) this library has made since it was
+ * loaded, its own and nut_malloc's (no reference counterpart: a
+ * diagnostic, for checking that nut_decode_noalloc allocates nothing). */
+int nut_device_allocations(unsigned long long *count);
 int nut_memcpy_h2d(void *d_dst, const void *src, size_t bytes);
 int nut_memcpy_d2h(void *dst, const void *d_src, size_t bytes);
 /* Device-to-device copy (synchronous); also the known-size copy that
@@ -211,12 +215,13 @@ int nut_kv_write_positions(nut_kvcache *kv, size_t begin, size_t end,
  * [dim] to hidden (host, may be NULL) and increments the length. */
 int nut_decode(nut_model *m, nut_kvcache *kv, int token, float *hidden);
 /* nut_decode without allocating (no reference counterpart): for callers
- * that cannot call hipMalloc (code under HIP graph capture, tight serving
- * loops, harnesses that forbid it). Same validation and result as
- * nut_decode on the step kernels (NUT_PATH_STEPS); the split-attention
- * partials and arrival counters live in a per-device 2 MiB scratch array
- * instead of model-owned allocations, and the hidden state goes to the
- * device pointer d_hidden (may be NULL). Limit: heads x splits x
+ * that cannot call hipMalloc (tight serving loops, harnesses that forbid
+ * it). It allocates nothing, but it is not itself capturable: it runs
+ * eagerly on the model's own stream and synchronizes it before returning.
+ * Same validation and result as nut_decode on the step kernels
+ * (NUT_PATH_STEPS); the split-attention partials and arrival counters live
+ * in a per-device 2 MiB scratch array instead of model-owned allocations,
+ * and the hidden state goes to the device pointer d_hidden (may be NULL). Limit: heads x splits x
  * (head_dim + 2) words of 8 bytes plus 2 x heads counters must fit 2 MiB,
  * else NUT_EINVAL (TinyLlama needs 0.55 MiB, Llama-2-7B 0.27). Every call
  * on one GPU shares that GPU's array and clears it first: calls that

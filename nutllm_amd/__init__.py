@@ -104,6 +104,7 @@ _SIGS = {
     "nut_set_device": (C.c_int, [C.c_int]),
     "nut_malloc": (C.c_int, [_P, _SZ]),
     "nut_free": (C.c_int, [_P]),
+    "nut_device_allocations": (C.c_int, [_P]),
     "nut_memcpy_h2d": (C.c_int, [_P, _P, _SZ]),
     "nut_memcpy_d2h": (C.c_int, [_P, _P, _SZ]),
     "nut_memcpy_d2d": (C.c_int, [_P, _P, _SZ]),
@@ -237,6 +238,13 @@ def token_tag_base(launch_count):
 
 
 # ---------------------------------------------------------------- device --
+
+def device_allocations():
+    """hipMalloc calls the library has made since it was loaded."""
+    n = C.c_ulonglong(0)
+    check(lib().nut_device_allocations(C.byref(n)))
+    return n.value
+
 
 def device_count():
     n = C.c_int(0)

@@ -17,13 +17,22 @@
 //   * a QuantizedModelWeights is uploaded at its first use, keyed by its
 //     address and a fingerprint of its storage; a QuantizedMatrix or a
 //     classifier Matrix likewise;
-//   * a KVCache gets a device twin. Rows the device writes are copied back
-//     into the host cache, so KVCache::key()/value()/length() read what the
-//     reference would hold (to the fp32 bar, rel-L2 1e-5); rows the host
-//     cache gained some other way (KVCache::store + set_length) are uploaded
-//     before the next device step.
+//   * a KVCache gets a device twin, made for the cache's configuration and
+//     remade when a cache of another configuration turns up at the address.
+//     Rows the device writes are copied back into the host cache, so
+//     KVCache::key()/value()/length() read what the reference would hold
+//     (to the fp32 bar, rel-L2 1e-5); rows the host cache gained some other
+//     way (KVCache::store + set_length) are uploaded before the next device
+//     step. A fingerprint of the first and last shared rows catches a new
+//     cache at a reused address and a reset; rows the host rewrites inside
+//     the shared run (KVCache::store below length()) are not detected: call
+//     nutgpu_release_cache(cache) after such a rewrite. At most kMaxTwins
+//     twins are kept; the least recently used one is dropped beyond that
+//     (its cache uploads every row at its next use).
 // nutgpu_release_device_state() drops every device copy: call it before
 // changing or freeing host weights that were used here.
+// nutgpu_release_cache(cache) drops one cache's twin: call it before the
+// cache is destroyed, or after rewriting its rows on the host.
 #include <algorithm>
 #include <chrono>
 #include <cstdint>
@@ -44,6 +53,8 @@
 #include "nutllm_hip.h"
 
 void nutgpu_release_device_state();
+void nutgpu_release_cache(const KVCache &cache);
+size_t nutgpu_cache_twins();
 
 namespace {
 
@@ -231,16 +242,44 @@ nut_model *device_model(const QuantizedModelWeights &w)
 
 // --------------------------------------------------------------- KV cache --
 
-// The device twin of a host KVCache, the positions both hold alike, and a
-// fingerprint of the host rows at the ends of that run (a different cache
-// at a reused address, or rows rewritten on the host, shows up as a
-// different value and makes the next use upload every row again).
+// The device twin of a host KVCache: the configuration it was made for,
+// the positions both hold alike, a fingerprint of the host rows at the ends
+// of that run (a different cache at a reused address, or a reset, shows up
+// as a different value and makes the next use upload every row again), and
+// when it was last used.
 struct Twin {
     nut_kvcache *kv = nullptr;
+    nut_config config{};
     size_t synced = 0;
     uint64_t print = 0;
+    uint64_t used = 0;
 };
 std::map<const KVCache *, Twin> g_caches;
+uint64_t g_cache_clock = 0;
+constexpr size_t kMaxTwins = 8;
+
+bool same_config(const nut_config &a, const nut_config &b)
+{
+    return a.layers == b.layers && a.heads == b.heads && a.dim == b.dim &&
+           a.head_dim == b.head_dim && a.ffn_dim == b.ffn_dim && a.vocab_size == b.vocab_size &&
+           a.max_seq == b.max_seq && a.eos_token == b.eos_token && a.kv_heads == b.kv_heads;
+}
+
+// Drops the least recently used twins other than `keep` until at most
+// kMaxTwins - 1 remain besides it.
+void evict_twins(const KVCache *keep)
+{
+    while (g_caches.size() >= kMaxTwins) {
+        auto oldest = g_caches.end();
+        for (auto it = g_caches.begin(); it != g_caches.end(); ++it)
+            if (it->first != keep && (oldest == g_caches.end() || it->second.used < oldest->second.used))
+                oldest = it;
+        if (oldest == g_caches.end())
+            return;
+        (void)nut_kv_destroy(oldest->second.kv);
+        g_caches.erase(oldest);
+    }
+}
 
 size_t kv_elements(const ModelConfig &c, size_t positions)
 {
@@ -266,10 +305,19 @@ uint64_t fingerprint(const KVCache &cache, const ModelConfig &c, size_t synced)
 // beyond what the twin shares are uploaded.
 nut_kvcache *device_cache(const KVCache &cache, const ModelConfig &c)
 {
+    const nut_config cfg = c_config(c);
+    if (g_caches.find(&cache) == g_caches.end())
+        evict_twins(&cache);
     Twin &t = g_caches[&cache];
+    t.used = ++g_cache_clock;
+    if (t.kv != nullptr && !same_config(t.config, cfg)) {
+        // another cache, of another configuration, at a reused address
+        (void)nut_kv_destroy(t.kv);
+        t.kv = nullptr;
+    }
     if (t.kv == nullptr) {
-        const nut_config cfg = c_config(c);
         check(nut_kv_create(&cfg, &t.kv));
+        t.config = cfg;
         t.synced = 0;
     } else if (t.print != fingerprint(cache, c, t.synced)) {
         t.synced = 0;
@@ -338,6 +386,22 @@ void check_decode(const QuantizedModelWeights &model, int token, const KVCache &
 }
 
 } // namespace
+
+void nutgpu_release_cache(const KVCache &cache)
+{
+    std::lock_guard<std::mutex> lock(g_lock);
+    const auto it = g_caches.find(&cache);
+    if (it == g_caches.end())
+        return;
+    (void)nut_kv_destroy(it->second.kv);
+    g_caches.erase(it);
+}
+
+size_t nutgpu_cache_twins()
+{
+    std::lock_guard<std::mutex> lock(g_lock);
+    return g_caches.size();
+}
 
 void nutgpu_release_device_state()
 {

@@ -71,6 +71,15 @@ int nut_malloc(void **d_ptr, size_t bytes)
         nut::require(d_ptr != nullptr, NUT_EINVAL, "malloc: null output");
         nut::ensure_device();
         nut::hip_check(hipMalloc(d_ptr, bytes == 0 ? 1 : bytes), "hipMalloc");
+        nut::count_device_allocation();
+    });
+}
+
+int nut_device_allocations(unsigned long long *count)
+{
+    return nut::guarded([&]() {
+        nut::require(count != nullptr, NUT_EINVAL, "device allocations: null output");
+        *count = nut::device_allocations();
     });
 }
 

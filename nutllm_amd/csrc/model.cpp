@@ -7,6 +7,7 @@
 #include "persistent.hpp"
 #include "prefill.hpp"
 #include "sample.hpp"
+#include "host/nucleus.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -574,10 +575,10 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     a.long_attention =
         start + n_iter > size_t(token_kernel_max_positions(m.type, s)) ? 1 : 0;
     {
-        // every word of this launch's write-once exchanges unset (0xffffffff);
-        // the buffer grows to the largest launch so far
+        // every word of the write-once ring unset (0xffffffff) when the
+        // launch starts; the ring's size does not depend on n_iter
         const bool wide = wide_kernel_positions(m.type, s) > 0;
-        const size_t floats = token_once_floats(s, wide, m.config.layers, n_iter);
+        const size_t floats = token_once_floats(s, wide);
         if (floats * sizeof(float) > m.exchange_once.bytes()) {
             m.exchange_once.release();
             m.exchange_once.allocate(floats * sizeof(float));
@@ -897,12 +898,12 @@ void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
         launch_classifier(s, m.hidden.as<float>(), m.final_norm.as<float>(), m.output_weights(),
                           m.logits.as<float>(), m.part_val.as<float>(), m.part_idx.as<int>(),
                           state, m.stream);
-        float *sorted_p = nullptr;
+        float *sorted_p = nullptr, *token_p = nullptr;
         int *sorted_ids = nullptr, *bad = nullptr;
         double *block_totals = nullptr;
         const int nt = sample_sort(m.logits.as<float>(), vocab, m.part_val.as<float>(), parts,
                                    temperature, m.sample_ws.get(), &sorted_p, &sorted_ids,
-                                   &block_totals, &bad, m.stream);
+                                   &token_p, &block_totals, &bad, m.stream);
         totals.resize(nt);
         int bad_host = 0;
         hip_check(hipMemcpyAsync(totals.data(), block_totals, nt * sizeof(double),
@@ -921,26 +922,42 @@ void generate_sampled(nut_model &m, const int *prompt, size_t prompt_len,
             fail(NUT_ERUNTIME, "sampling: zero probability mass");
         // the nucleus: the sorted prefix until its mass reaches top_p of the
         // total (src/generate.cpp:63-68), read in chunks
-        const double cutoff = top_p * total;
-        double nucleus = 0.0;
-        size_t taken = 0;
         p.clear();
         ids.clear();
-        do {
-            if (taken == p.size()) {
+        auto sorted = [&](size_t i) {
+            if (i == p.size()) {
                 const size_t n = std::min(kChunk, size_t(vocab) - p.size());
                 p.resize(p.size() + n);
                 ids.resize(ids.size() + n);
-                hip_check(hipMemcpy(p.data() + taken, sorted_p + taken, n * sizeof(float),
+                hip_check(hipMemcpy(p.data() + i, sorted_p + i, n * sizeof(float),
                                     hipMemcpyDeviceToHost),
                           "hipMemcpy to host");
-                hip_check(hipMemcpy(ids.data() + taken, sorted_ids + taken, n * sizeof(int),
+                hip_check(hipMemcpy(ids.data() + i, sorted_ids + i, n * sizeof(int),
                                     hipMemcpyDeviceToHost),
                           "hipMemcpy to host");
             }
-            nucleus += p[taken];
-            taken++;
-        } while (taken < size_t(vocab) && nucleus < cutoff);
+            return double(p[i]);
+        };
+        // The block sums and the reference's sum in token order round
+        // differently: each is within (vocab - 1) 2^-53 of the exact sum,
+        // relative to it. When a total that far off could move the cut,
+        // the total is formed in token order, as the reference forms it.
+        const double slack = total * double(vocab) * 0x1p-52 * 1.01;
+        double nucleus = 0.0;
+        bool ambiguous = false;
+        size_t taken = nucleus_count(sorted, size_t(vocab), top_p, total, slack, nucleus,
+                                     ambiguous);
+        if (ambiguous) {
+            std::vector<float> in_order(static_cast<size_t>(vocab));
+            hip_check(hipMemcpy(in_order.data(), token_p, in_order.size() * sizeof(float),
+                                hipMemcpyDeviceToHost),
+                      "hipMemcpy to host");
+            double sequential = 0.0;
+            for (float q : in_order)
+                sequential += q;
+            taken = nucleus_count(sorted, size_t(vocab), top_p, sequential, 0.0, nucleus,
+                                  ambiguous);
+        }
         // the draw and the walk (src/generate.cpp:70-79)
         std::uniform_real_distribution<double> draw(0.0, nucleus);
         const double target = draw(rng);

@@ -12,9 +12,11 @@
 // Phases exchange activations through HBM in words written with agent-scope
 // (sc1) stores; a consumer polls the words it needs until they hold the
 // producing phase's output, so the flag is the data itself and no cache-wide
-// writeback or invalidate is needed. With the fused attention every exchange
-// of a launch has write-once 32-bit words of its own (unset until written);
-// split attention reuses its words with 64-bit (value, tag) words.
+// writeback or invalidate is needed. Every exchange of a (token, layer) step
+// has write-once 32-bit words of its own (unset until written) in a ring of
+// three step slices, each re-armed by its producers once every consumer has
+// read it; split attention's per-position partials and the argmax reuse
+// their words with 64-bit (value, tag) words.
 //
 // Latency hiding: before a workgroup waits for a phase's input, it starts
 // LDS DMA (global_load_lds_dwordx4) of that phase's weight rows — and, for
@@ -123,6 +125,9 @@ struct Geo {
                   "fused attention: a wave per query head, a lane per dim and per position");
     static_assert(DIM % WGS_G == 0 && WO_BLK == 16 && WO_WG == 4 * kWaves && WO_SEG % 16 == 0,
                   "fused attention Wo: four rows of 16 blocks per wave");
+    static_assert(GR_WG <= kWave && WO_WG <= kWave && ROWS_GU / 2 <= kWave &&
+                      ROWS_DN <= kWave && ROWS_WO <= kWave && HD / 8 == kWaves,
+                  "a workgroup's words of each exchange re-armed by one wave");
 };
 
 // ------------------------------------------------- split attention --
@@ -262,6 +267,7 @@ __device__ void split_attention(int cnt, int ag, const float *kst, const float *
 // LDS DMA of `rows` segments of `seg` bytes (a multiple of 16), row r at
 // src + r * stride, packed in LDS (segment r at lds_dst + r * seg); issued
 // as dma() is, with the same completion.
+template <int POLICY = kStreamPolicy>
 __device__ __forceinline__ void dma_segments(uint8_t *lds_dst, const uint8_t *src, int rows,
                                              int seg, int stride)
 {
@@ -275,7 +281,7 @@ __device__ __forceinline__ void dma_segments(uint8_t *lds_dst, const uint8_t *sr
                 (const __attribute__((address_space(1))) void *)(src + size_t(row) * stride +
                                                                  g * 16),
                 (__attribute__((address_space(3))) void *)(lds_dst + i * 1024), 16, 0,
-                kStreamPolicy);
+                POLICY);
     }
 }
 
@@ -357,16 +363,24 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         return reinterpret_cast<const uint16_t *>(
             a.weights + size_t(layer) * G::LAY.bytes + G::LAY.scales[m]);
     };
+    // matrix m of layer `layer` stays in the memory-side cache (default
+    // policy) instead of streaming (non-temporal)
+    auto resident = [&](int layer, int m) {
+        return layer < a.resident_layers && ((a.resident_mask >> m) & 1) != 0;
+    };
     auto stage = [&](uint8_t *region, int rows, int rb, int sb, int layer,
                      int m, int lo, int hi, int first) {
         if (hi <= lo)
             return;
-        dma(region + first * rb, wdata(layer, m) + size_t(lo) * rb,
-            (hi - lo) * rb);
-        dma(region + rows * rb + first * sb,
-            reinterpret_cast<const uint8_t *>(wscales(layer, m)) +
-                size_t(lo) * sb,
-            (hi - lo) * sb);
+        const uint8_t *d = wdata(layer, m) + size_t(lo) * rb;
+        const uint8_t *sc = reinterpret_cast<const uint8_t *>(wscales(layer, m)) + size_t(lo) * sb;
+        if (resident(layer, m)) {
+            dma<0>(region + first * rb, d, (hi - lo) * rb);
+            dma<0>(region + rows * rb + first * sb, sc, (hi - lo) * sb);
+        } else {
+            dma(region + first * rb, d, (hi - lo) * rb);
+            dma(region + rows * rb + first * sb, sc, (hi - lo) * sb);
+        }
     };
     // The group's rows [lo, hi) are q rows of its heads, then its k and v
     // rows.
@@ -422,9 +436,9 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
     constexpr int ON_WO = G::DIM + 2 * G::KVD, ON_GU = ON_WO + G::KVH * G::DIM;
     constexpr int ON_DN = ON_GU + G::FFN;
     constexpr int ONCE = ON_DN + G::DIM;
-    auto once = [&](int it, int layer, int part) {
-        return a.x_once + (size_t(it) * a.layer_count + layer) * ONCE + part;
-    };
+    // the ring slice of the current (iteration, layer) step, advanced by one
+    // per step (once_slice(it, layer, layer_count))
+    int slice = 0;
 
     int count = 0, done = 0, last_token = 0;
     // Write-once words of the hidden state the next classifier reads; null
@@ -500,6 +514,9 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         for (int l = 0; l < a.layer_count; l++) {
             float *kc = a.k_cache + l * kv_layer;
             float *vc = a.v_cache + l * kv_layer;
+            // this step's write-once words, and the previous step's
+            float *xo = a.x_once + size_t(slice) * ONCE;
+            float *xp = a.x_once + size_t(slice == 0 ? kOnceRing - 1 : slice - 1) * ONCE;
 
             // ---------------------------------------------- phase A: qkv --
             // RoPE factors of this wave's first pair, read before the wait.
@@ -529,7 +546,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = e.store(h_raw);
                 dma_wait();
             } else {
-                sq = take_once<G::DIM, false, PollDelay<LONG>::A>(once(it, l - 1, ON_DN), h_raw,
+                sq = take_once<G::DIM, false, PollDelay<LONG>::A>(xp + ON_DN, h_raw,
                                                                    error);
             }
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
@@ -554,8 +571,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                             e0 = fmaf(even, cs.x, -(odd * cs.y));
                             e1 = fmaf(even, cs.y, odd * cs.x);
                         }
-                        put_once(once(it, l, 0) + row, e0);
-                        put_once(once(it, l, 0) + row + 1, e1);
+                        put_once(xo + row, e0);
+                        put_once(xo + row + 1, e1);
                         if (which > 0) {
                             float *cache = (which == 1 ? kc : vc) +
                                            (size_t(head) * a.max_seq + pos) * G::HD + d;
@@ -599,7 +616,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
             // anything later is published)
-            take_once<G::GR, false, PollDelay<LONG>::B>(once(it, l, 0) + grp * G::GR, qkv, error);
+            take_once<G::GR, false, PollDelay<LONG>::B>(xo + grp * G::GR, qkv, error);
             if (LONG) {
                 // the new position's K/V row, when it falls in this unit
                 if (pos >= ap0 && pos < ap1)
@@ -619,11 +636,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             __syncthreads();
             mark(it, 5 + 13 * l);
             if constexpr (LONG) {
-                split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, once(it, l, ON_WO),
+                split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, xo + ON_WO,
                                    tag, error);
                 tag++;
                 // the whole context, as digits for the Wo rows
-                take_once<G::DIM, false, PollDelay<true>::CONTEXT>(once(it, l, ON_WO), qkv, error);
+                take_once<G::DIM, false, PollDelay<true>::CONTEXT>(xo + ON_WO, qkv, error);
                 quartet_digits<G::QT>(reinterpret_cast<const float4 *>(qkv)[threadIdx.x],
                                       threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             } else {
@@ -684,7 +701,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     slot(G::ROWS_WO, G::RB_DIM, G::SB_DIM, r, d, s, r2);
                     const float y = row_dot_lds<G::QT, G::CPL_DIM>(d, s, xl, xsc, G::BLK_DIM);
                     if (lane == 0)
-                        put_once(once(it, l, ON_WO) + G::DIM + wo_b + r, h_raw[wo_b + r] + y);
+                        put_once(xo + ON_WO + G::DIM + wo_b + r, h_raw[wo_b + r] + y);
                 }
             } else {
                 // Wo partial sums over the group's context columns: wave w
@@ -700,7 +717,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 const float y = row16_sum(half_bits_to_float(s[b]) * xsc[b] *
                                           dot_block_digits<G::QT>(d, b, dg));
                 if (b == 0)
-                    put_once(once(it, l, ON_WO) + grp * G::DIM + gj * G::WO_WG + r, y);
+                    put_once(xo + ON_WO + grp * G::DIM + gj * G::WO_WG + r, y);
             }
             tag++;
             // every wave is past attention (region 1) and past its reads of
@@ -712,11 +729,29 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
 
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
+            // Every workgroup has taken the previous step's h after Wo, so
+            // every word of the step before it has been read: this
+            // workgroup's words of that step go back to kUnset for the
+            // slice's next use (this take retires the stores).
+            if (it * a.layer_count + l >= 2) {
+                float *xr = a.x_once + size_t(slice >= 2 ? slice - 2 : slice + kOnceRing - 2) * ONCE;
+                rearm_words(xr + grp * G::GR + gj * G::GR_WG, G::GR_WG, 0);
+                if constexpr (LONG) {
+                    // merged context values, then h after Wo
+                    rearm_words(xr + ON_WO + (blockIdx.x >> 3) * G::HD + (blockIdx.x & 7) * 8, 8,
+                                1);
+                    rearm_words(xr + ON_WO + G::DIM + wo_b, wo_e - wo_b, 4);
+                } else {
+                    rearm_words(xr + ON_WO + grp * G::DIM + gj * G::WO_WG, G::WO_WG, 1);
+                }
+                rearm_words(xr + ON_GU + gu_b, gu_e - gu_b, 2);
+                rearm_words(xr + ON_DN + dn_b, dn_e - dn_b, 3);
+            }
             if constexpr (LONG)
-                sq = take_once<G::DIM, false, PollDelay<LONG>::C>(once(it, l, ON_WO) + G::DIM,
+                sq = take_once<G::DIM, false, PollDelay<LONG>::C>(xo + ON_WO + G::DIM,
                                                                   h_raw, error);
             else
-                sq = take_once_sum<G::DIM, G::KVH, PollDelay<LONG>::C>(once(it, l, ON_WO), h_raw,
+                sq = take_once_sum<G::DIM, G::KVH, PollDelay<LONG>::C>(xo + ON_WO, h_raw,
                                                                       error);
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 9 + 13 * l);
@@ -731,7 +766,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const float g = row_dot<G::QT>(dg, sg, x, G::BLK_DIM);
                     const float u = row_dot<G::QT>(du, su, x, G::BLK_DIM);
                     if (lane == 0) {
-                        put_once(once(it, l, ON_GU) + gu_b + pair, g / (1.0f + expf(-g)) * u);
+                        put_once(xo + ON_GU + gu_b + pair, g / (1.0f + expf(-g)) * u);
                     }
                 }
             }
@@ -742,7 +777,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
-            take_once<G::FFN, true, PollDelay<LONG>::D>(once(it, l, ON_GU), xs, error);
+            take_once<G::FFN, true, PollDelay<LONG>::D>(xo + ON_GU, xs, error);
             block_sums(xs, xsc, G::FFN);
             mark(it, 12 + 13 * l);
             {
@@ -754,7 +789,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     const float y = row_dot_floats<G::QT, G::CPL_FFN>(d, s, xs, xsc, G::BLK_FFN);
                     if (lane == 0) {
                         const float v = h_raw[dn_b + r] + y;
-                        put_once(once(it, l, ON_DN) + dn_b + r, v);
+                        put_once(xo + ON_DN + dn_b + r, v);
                         if (last && it + 1 == a.n_iter)
                             a.hidden_out[dn_b + r] = v;
                     }
@@ -764,7 +799,8 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 if (!last)
                     stage_qkv(l + 1);
             }
-            hidden_once = once(it, l, ON_DN);
+            hidden_once = xo + ON_DN;
+            slice = slice + 1 == kOnceRing ? 0 : slice + 1;
             tag++;
             mark(it, 14 + 13 * l);
         }

@@ -30,7 +30,8 @@ struct TokenArgs {
     // The q/k/v (or the wide kernel's context), h and act exchanges in
     // write-once words (token_once_floats of them, every word kUnset =
     // 0xffffffff when the launch starts), iteration it and layer l at
-    // x_once + (it * layer_count + l) * token_once_stride.
+    // x_once + once_slice(it, l, layer_count) * token_once_stride (the
+    // kernels advance the slice index by one per step).
     float *x_once;
     // Long contexts (long_attention != 0): attention is split over the
     // workgroups; x_apart holds each workgroup's partial (m, l, o) for the
@@ -52,6 +53,12 @@ struct TokenArgs {
     // timeline_cap entries per workgroup.
     unsigned long long *timeline;
     int timeline_cap, timeline_wgs;
+    // Weight rows of matrix m (bit m: q, k, v, o, gate, up, down) of layers
+    // below resident_layers are staged with the default cache policy, so
+    // they stay in the memory-side cache from token to token; the rest
+    // stream (non-temporal).
+    int resident_layers;
+    unsigned resident_mask;
     int layer_count, vocab, max_seq, eos;
     int start_len, n_iter, classify;
     float attn_scale;
@@ -74,9 +81,30 @@ inline size_t token_once_stride(const DecodeShape &s, bool wide)
     return size_t(s.dim) * (2 + s.kv_heads) + 2 * size_t(s.kv_heads) * s.head_dim + s.ffn_dim;
 }
 
-inline size_t token_once_floats(const DecodeShape &s, bool wide, size_t layers, size_t n_iter)
+// The write-once words form a ring of kOnceRing slices, one per (iteration,
+// layer) step: step u = it * layers + l uses slice u % kOnceRing. At the
+// start of phase C of step u + 2, before its take of that step's h after
+// Wo, each workgroup sets the words it published in step u back to kUnset:
+// it has taken the h after Wo of step u + 1, into which every workgroup
+// publishes only after it has taken every exchange of step u, so no
+// consumer still polls them. The take that follows retires the re-arming
+// stores (its closing s_waitcnt vmcnt(0)) before the workgroup publishes
+// its activation of step u + 2, and every consumer takes that activation
+// before it polls a word of step u + 3, the slice's next use, so it finds
+// kUnset there until the new value; the workgroup's own words of step
+// u + 3 come after its re-arm in program order. tests/test_cpu_once_ring.py
+// replays the protocol and shows that two slices would not do. The ring's
+// size is independent of the tokens a launch decodes.
+constexpr int kOnceRing = 3;
+
+__host__ __device__ inline int once_slice(int it, int layer, int layers)
 {
-    return n_iter * layers * token_once_stride(s, wide);
+    return (it * layers + layer) % kOnceRing;
+}
+
+inline size_t token_once_floats(const DecodeShape &s, bool wide)
+{
+    return kOnceRing * token_once_stride(s, wide);
 }
 
 // Exchange tags. Every exchange word is (tag << 32) | value, and a launch

@@ -1,4 +1,5 @@
 // runtime.cpp — HIP error mapping, device selection and buffers.
+#include <atomic>
 #include "runtime.hpp"
 
 #include <cstring>
@@ -56,12 +57,21 @@ void ensure_device()
     select_device(g_device);
 }
 
+namespace {
+std::atomic<unsigned long long> g_allocations{0};
+}
+
+unsigned long long device_allocations() { return g_allocations.load(); }
+
+void count_device_allocation() { g_allocations.fetch_add(1); }
+
 void DeviceBuffer::allocate(size_t bytes)
 {
     release();
     if (bytes == 0)
         bytes = 1;
     hip_check(hipMalloc(&ptr_, bytes), "hipMalloc");
+    count_device_allocation();
     bytes_ = bytes;
 }
 

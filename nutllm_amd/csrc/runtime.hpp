@@ -25,6 +25,11 @@ void check_launch(const char *what);
 // NUT_EDEVICE when there is none.
 void ensure_device();
 
+// Device allocations made by this library since it was loaded (every
+// hipMalloc it issues: DeviceBuffer::allocate and nut_malloc).
+unsigned long long device_allocations();
+void count_device_allocation();
+
 // RAII device allocation.
 class DeviceBuffer {
 public:

@@ -109,7 +109,7 @@ size_t sample_workspace_bytes(int vocab) { return layout_of(vocab).total; }
 
 int sample_sort(const float *logits, int vocab, const float *part_val, int parts,
                 float temperature, void *workspace, float **sorted_p, int **sorted_ids,
-                double **totals, int **bad, hipStream_t stream)
+                float **token_p, double **totals, int **bad, hipStream_t stream)
 {
     const Layout l = layout_of(vocab);
     char *base = static_cast<char *>(workspace);
@@ -131,6 +131,8 @@ int sample_sort(const float *logits, int vocab, const float *part_val, int parts
               "sampling: radix sort");
     *sorted_p = reinterpret_cast<float *>(keys_out);
     *sorted_ids = ids_out;
+    // the sort reads its input keys and leaves them as they were
+    *token_p = reinterpret_cast<float *>(keys);
     *totals = tot;
     *bad = flag;
     return kBlocks;

@@ -47,17 +47,31 @@ __device__ __forceinline__ void put(uint64_t *p, float v, unsigned tag)
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Write-once words: an exchange that owns its words alone within a launch
-// (TokenArgs::x_once) publishes plain 32-bit values into words the host set
-// to kUnset before the launch. Each word goes from kUnset to its value once,
-// so the value is its own flag at half the bytes of a tagged word, and a
-// 64-bit poll of two words needs no atomicity across them. kUnset is a NaN
-// that put_once never writes: it publishes every NaN as the canonical one.
+// Write-once words: an exchange that owns its words alone within a step of
+// a launch (TokenArgs::x_once: a ring of slices, persistent.hpp) publishes
+// plain 32-bit values into words that hold kUnset (set by the host before
+// the launch, or re-armed by their producer once every consumer has read
+// them). Each word goes from kUnset to its value once per use, so the value
+// is its own flag at half the bytes of a tagged word, and a 64-bit poll of
+// two words needs no atomicity across them. kUnset is a NaN that put_once
+// never writes: it publishes every NaN as the canonical one.
 constexpr uint32_t kUnset = 0xffffffffu;
 
 __device__ __forceinline__ void put_once(float *p, float v)
 {
     store_coherent(p, v != v ? __uint_as_float(0x7fc00000u) : v);
+}
+
+// Re-arming (the ring of write-once slices, persistent.hpp: kOnceRing):
+// wave w sets the n <= kWave words at p back to kUnset. The next take's
+// closing s_waitcnt vmcnt(0) retires the stores.
+__device__ __forceinline__ void rearm_words(float *p, int n, int w)
+{
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x / kWave) == w) {
+        const int lane = threadIdx.x & (kWave - 1);
+        if (lane < n)
+            store_coherent(p + lane, __uint_as_float(kUnset));
+    }
 }
 
 __device__ __forceinline__ bool unset_pair(uint64_t w)
@@ -120,6 +134,7 @@ __device__ __forceinline__ int wave_index()
 // for the TinyLlama shape).
 constexpr int kStreamPolicy = 2;
 
+template <int POLICY = kStreamPolicy>
 __device__ __forceinline__ void dma(void *lds_dst, const void *src, int bytes)
 {
     const int lane = threadIdx.x & (kWave - 1);
@@ -132,7 +147,7 @@ __device__ __forceinline__ void dma(void *lds_dst, const void *src, int bytes)
                     static_cast<const char *>(src) + off),
                 (__attribute__((address_space(3))) void *)(
                     static_cast<char *>(lds_dst) + (i << 10)),
-                16, 0, kStreamPolicy);
+                16, 0, POLICY);
     }
 }
 

@@ -71,6 +71,8 @@ struct Wide {
                   "sixteen head dims per workgroup: one q, k and v pair per wave");
     static_assert(DIM % kGrid == 0 && ROWS == 2 * kWaves, "one Wo / W2 row pair per wave");
     static_assert(FFN % kGrid == 0, "gate/up pairs split evenly over workgroups");
+    static_assert(SLICE <= kWave && ROWS <= kWave && GU <= kWave,
+                  "a workgroup's words of each exchange re-armed by one wave");
     static_assert((GU - GU_LDS) % kWaves == 0, "gate/up pairs in registers split evenly over waves");
     static_assert(DIM % (4 * kThreads) == 0 && NMAX % kThreads == 0,
                   "whole quartets and positions per thread");
@@ -471,8 +473,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
     // after Wo, act, h after W2 (the partial scores stay tagged).
     constexpr int X_WO = G::DIM, X_ACT = 2 * G::DIM, X_DN = 2 * G::DIM + G::FFN;
     constexpr int X_STRIDE = X_DN + G::DIM;
-    auto once = [&](int it, int layer, int part) {
-        return fresh(a.x_once) + (size_t(it) * a.layer_count + layer) * X_STRIDE + part;
+    // the ring slice of the current (iteration, layer) step, advanced by one
+    // per step (once_slice(it, layer, layer_count)); this step's words and
+    // the previous step's
+    int slice = 0;
+    auto once = [&](int part) { return fresh(a.x_once) + size_t(slice) * X_STRIDE + part; };
+    // the words of two steps back, which phase C re-arms
+    auto once_back2 = [&](int part) {
+        return fresh(a.x_once) + size_t(slice >= 2 ? slice - 2 : slice + kOnceRing - 2) * X_STRIDE +
+               part;
     };
 
     int count = 0, done = 0, last_token = 0;
@@ -741,13 +750,13 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
 #pragma unroll
                 for (int w = 0; w < kWaves; w++)
                     t += ctxp[w * G::SLICE + threadIdx.x];
-                put_once(once(it, l, 0) + qkv0 + threadIdx.x, t / total);
+                put_once(once(0) + qkv0 + threadIdx.x, t / total);
             }
             tag++;
             mark(it, 5 + 13 * l);
 
             // ------------------------------------ Wo rows + residual --
-            take_once<G::DIM, false, kWidePollDelayContext, true>(once(it, l, 0), hbuf, error);
+            take_once<G::DIM, false, kWidePollDelayContext, true>(once(0), hbuf, error);
             {
                 float4 ones[G::XQ];
 #pragma unroll
@@ -762,8 +771,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 res0 += y[0];
                 res1 += y[1];
                 if (lane == 0) {
-                    put_once(once(it, l, X_WO) + ra, res0);
-                    put_once(once(it, l, X_WO) + rb, res1);
+                    put_once(once(X_WO) + ra, res0);
+                    put_once(once(X_WO) + rb, res1);
                 }
             }
             tag++;
@@ -789,7 +798,17 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                                    wscales(5, r, G::SB_DIM));
             }
             load_quartets(nw, norm(l, true));
-            sq = take_once<G::DIM, false, 0, true>(once(it, l, X_WO), hbuf, error);
+            // Every workgroup has taken the previous step's h after Wo, so
+            // every word of the step before it has been read: this
+            // workgroup's words of that step go back to kUnset for the
+            // slice's next use (this take retires the stores).
+            if (it * a.layer_count + l >= 2) {
+                rearm_words(once_back2(0) + qkv0, G::SLICE, 0);
+                rearm_words(once_back2(X_WO) + row0, G::ROWS, 1);
+                rearm_words(once_back2(X_ACT) + gu0, G::GU, 2);
+                rearm_words(once_back2(X_DN) + row0, G::ROWS, 3);
+            }
+            sq = take_once<G::DIM, false, 0, true>(once(X_WO), hbuf, error);
             stage_quartets<G::QT, G::XQ>(hbuf, nw, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 8 + 13 * l);
             {
@@ -799,7 +818,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 for (int i = 0; i < G::NREG; i++)
                     if (lane == 0) {
                         const float g = y[2 * i], u = y[2 * i + 1];
-                        put_once(once(it, l, X_ACT) + gu0 + G::GU_LDS + wave + kWaves * i,
+                        put_once(once(X_ACT) + gu0 + G::GU_LDS + wave + kWaves * i,
                                  g / (1.0f + expf(-g)) * u);
                     }
             }
@@ -819,7 +838,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 for (int i = 0; i < G::NLDS; i++)
                     if (i < n_lds && lane == 0) {
                         const float g = y[2 * i], u = y[2 * i + 1];
-                        put_once(once(it, l, X_ACT) + gu0 + wave + kWaves * i,
+                        put_once(once(X_ACT) + gu0 + wave + kWaves * i,
                                  g / (1.0f + expf(-g)) * u);
                     }
             }
@@ -836,21 +855,22 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                        wscales(6, ra, G::SB_FFN));
             wd[1].load(layer_rsrc<G>(a.weights, l), wdata(6, rb, G::RB_FFN),
                        wscales(6, rb, G::SB_FFN));
-            take_once<G::FFN, true, 0, true>(once(it, l, X_ACT), act, error);
+            take_once<G::FFN, true, 0, true>(once(X_ACT), act, error);
             block_sums(act, xsc, G::FFN);
             mark(it, 10 + 13 * l);
             res0 += regs_dot_floats(wd[0], act, xsc, G::BLK_FFN);
             res1 += regs_dot_floats(wd[1], act, xsc, G::BLK_FFN);
             if (lane == 0) {
-                put_once(once(it, l, X_DN) + ra, res0);
-                put_once(once(it, l, X_DN) + rb, res1);
+                put_once(once(X_DN) + ra, res0);
+                put_once(once(X_DN) + rb, res1);
                 if (last && it + 1 == a.n_iter) {
                     a.hidden_out[ra] = res0;
                     a.hidden_out[rb] = res1;
                 }
             }
             hidden_tag = tag;
-            hidden_once = once(it, l, X_DN);
+            hidden_once = once(X_DN);
+            slice = slice + 1 == kOnceRing ? 0 : slice + 1;
             tag++;
             mark(it, 11 + 13 * l);
             // every wave is past its reads of the activation, which the next

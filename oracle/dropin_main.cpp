@@ -20,6 +20,8 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <memory>
+#include <new>
 #include <random>
 #include <stdexcept>
 #include <string>
@@ -45,6 +47,8 @@ void cpu_matvec_quantized_threaded(const QuantizedMatrix &, const float *, float
 void cpu_matvec_threaded(const Matrix &, const float *, float *, size_t);
 void cpu_matmul_threaded(const Matrix &, const Matrix &, Matrix &, size_t);
 void nutgpu_release_device_state();
+void nutgpu_release_cache(const KVCache &cache);
+size_t nutgpu_cache_twins();
 
 namespace {
 
@@ -97,7 +101,7 @@ std::vector<float> uniform(std::mt19937 &rng, size_t n, float scale)
 
 // A two-layer model at a shape the device's fast step kernels run (head_dim
 // 64, two query heads per KV head), weights U(-0.05, 0.05) from mt19937.
-QuantizedModelWeights synthetic(QuantType type, unsigned seed)
+QuantizedModelWeights synthetic(QuantType type, unsigned seed, size_t max_seq = 96)
 {
     ModelConfig c;
     c.layers = 2;
@@ -106,7 +110,7 @@ QuantizedModelWeights synthetic(QuantType type, unsigned seed)
     c.head_dim = 64;
     c.ffn_dim = 512;
     c.vocab_size = 512;
-    c.max_seq = 96;
+    c.max_seq = max_seq;
     c.eos_token = 1;
     c.kv_heads = 2;
     std::mt19937 rng(seed);
@@ -163,6 +167,83 @@ void host_checks(const QuantizedModelWeights &model)
     expect_throw<std::invalid_argument>([&] { matmul_threaded(a, b, c, 1); },
                                         "threaded matmul: shape mismatch",
                                         "matmul_threaded rejects mismatched shapes");
+}
+
+// Hidden state of one more decode on `dev` against the same decode on the
+// CPU copy `cpu` of its cache.
+double decode_both(const QuantizedModelWeights &m, int token, KVCache &dev, KVCache &cpu)
+{
+    const std::vector<float> hd = decode_quantized_token(m, token, dev, 2);
+    const std::vector<float> hc = cpu_decode_quantized_token(m, token, cpu, 2);
+    return rel_l2(hd.data(), hc.data(), m.config.dim);
+}
+
+// The device twins of host caches: a cache of another configuration at a
+// reused address, an interior row rewritten on the host, more caches than
+// the adapter keeps twins for.
+void cache_twin_checks()
+{
+    const QuantizedModelWeights a = synthetic(QuantType::int8, 21, 96);
+    const QuantizedModelWeights b = synthetic(QuantType::int8, 22, 64);
+    const std::vector<int> prompt = {5, 9, 200, 17};
+    alignas(KVCache) unsigned char storage[sizeof(KVCache)];
+    {
+        KVCache *first = new (storage) KVCache(a.config);
+        KVCache cpu(a.config);
+        prefill_quantized(a, prompt, *first, 2);
+        cpu_prefill_quantized(a, prompt, cpu, 2);
+        const double e = decode_both(a, 33, *first, cpu);
+        first->~KVCache();
+        // no release call: the next cache at this address has another
+        // configuration (max_seq 64)
+        KVCache *second = new (storage) KVCache(b.config);
+        KVCache cpu_b(b.config);
+        prefill_quantized(b, prompt, *second, 2);
+        cpu_prefill_quantized(b, prompt, cpu_b, 2);
+        const double eb = decode_both(b, 34, *second, cpu_b);
+        expect(e <= 1e-5 && eb <= 1e-5,
+               "a cache of another configuration at a reused address gets a twin of its own");
+        nutgpu_release_cache(*second);
+        second->~KVCache();
+    }
+    {
+        // an interior row rewritten on the host, then the twin released
+        KVCache dev(a.config), cpu(a.config);
+        prefill_quantized(a, prompt, dev, 2);
+        cpu_prefill_quantized(a, prompt, cpu, 2);
+        const ModelConfig &c = a.config;
+        std::vector<float> k(c.effective_kv_heads() * c.head_dim, 0.25f),
+            v(c.effective_kv_heads() * c.head_dim, -0.5f);
+        for (KVCache *x : {&dev, &cpu}) {
+            const size_t length = x->length();
+            x->store(0, 1, k.data(), v.data());
+            x->set_length(length);
+        }
+        nutgpu_release_cache(dev);
+        expect(decode_both(a, 40, dev, cpu) <= 1e-5,
+               "after nutgpu_release_cache, a host rewrite inside the cache reaches the device");
+        nutgpu_release_cache(dev);
+    }
+    {
+        // more caches than twins: the least recently used twin is dropped,
+        // and its cache uploads every row at its next use
+        std::vector<std::unique_ptr<KVCache>> dev, cpu;
+        for (int i = 0; i < 10; i++) {
+            dev.emplace_back(new KVCache(a.config));
+            cpu.emplace_back(new KVCache(a.config));
+            prefill_quantized(a, {int(i + 2), 7}, *dev.back(), 2);
+            cpu_prefill_quantized(a, {int(i + 2), 7}, *cpu.back(), 2);
+        }
+        const size_t twins = nutgpu_cache_twins();
+        double worst = 0.0;
+        for (int i = 0; i < 10; i++)
+            worst = std::max(worst, decode_both(a, 100 + i, *dev[i], *cpu[i]));
+        expect(twins <= 8 && nutgpu_cache_twins() <= 8 && worst <= 1e-5,
+               "cache twins stay bounded (" + std::to_string(twins) +
+                   " after ten caches); evicted caches decode from a fresh upload");
+        for (auto &d : dev)
+            nutgpu_release_cache(*d);
+    }
 }
 
 void device_checks(const std::string &fixture)
@@ -260,6 +341,8 @@ void device_checks(const std::string &fixture)
         }
         expect(mv <= 1e-5, tag + ": matvec_quantized_threaded rel-L2 " + std::to_string(mv));
     }
+
+    cache_twin_checks();
 
     // the fp32 classifier matvec and the fp32 GEMM
     std::mt19937 rng(8);

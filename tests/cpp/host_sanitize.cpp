@@ -4,15 +4,21 @@
 // synthetic generator and the fp16 scale codec, each driven from several
 // caller threads at once, with every result compared bit for bit against a
 // serial run. Built from the sources by tests/cpp/Makefile (sanitize
-// target) and run by tests/test_cpu_host_sanitize.py.
+// target) and run by tests/test_cpu_host_sanitize.py. Also the sampled
+// loop's nucleus cut (host/nucleus.hpp) against the reference's order of
+// summation.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <functional>
+#include <random>
 #include <string>
 #include <thread>
 #include <vector>
 
+#include "host/nucleus.hpp"
 #include "nutllm_hip.h"
 
 // The C ABI's thread-local last-error message, as the library keeps it
@@ -67,10 +73,62 @@ std::vector<float> normal(uint64_t seed, uint64_t stream, size_t n, float sigma)
     return v;
 }
 
+// choose_token's nucleus (src/generate.cpp:63-68) with the total summed in
+// 128 strided blocks, as the device sums it, against the total summed in
+// token order, as the reference sums it: wherever nucleus_count does not
+// flag the cut as ambiguous, the count and the nucleus equal the ones the
+// token-order total gives (model.cpp recomputes the total in token order
+// for the flagged cuts).
+void nucleus_checks()
+{
+    std::mt19937 rng(17);
+    std::uniform_real_distribution<float> u01(0.0f, 1.0f);
+    int decided = 0, flagged = 0;
+    for (int trial = 0; trial < 600; trial++) {
+        const size_t n = 300 + rng() % 3000;
+        // spreads from a few e-folds to far below a double ulp of the total
+        const float spread = trial % 3 == 0 ? 80.0f : trial % 3 == 1 ? 12.0f : 3.0f;
+        std::vector<float> p(n);
+        for (float &x : p)
+            x = std::exp(-spread * u01(rng));
+        double sequential = 0.0;
+        for (float x : p)
+            sequential += x;
+        double blocks = 0.0;
+        for (size_t b = 0; b < 128; b++) {
+            double t = 0.0;
+            for (size_t i = b; i < n; i += 128)
+                t += p[i];
+            blocks += t;
+        }
+        std::vector<float> sorted(p);
+        std::sort(sorted.begin(), sorted.end(), std::greater<float>());
+        const float top_p = trial % 2 == 0 ? 1.0f : 0.05f + 0.95f * u01(rng);
+        auto next = [&](size_t i) { return double(sorted[i]); };
+        double nucleus_ref = 0.0, nucleus = 0.0;
+        bool unused = false, ambiguous = false;
+        const size_t ref = nut::nucleus_count(next, n, top_p, sequential, 0.0, nucleus_ref, unused);
+        const double slack = blocks * double(n) * 0x1p-52 * 1.01;
+        expect(std::fabs(blocks - sequential) <= slack, "nucleus: block total within slack");
+        const size_t got = nut::nucleus_count(next, n, top_p, blocks, slack, nucleus, ambiguous);
+        if (ambiguous) {
+            flagged++;
+        } else {
+            decided++;
+            expect(got == ref && nucleus == nucleus_ref,
+                   "nucleus: an unflagged cut equals the token-order total's");
+        }
+    }
+    expect(decided > 300, "nucleus: most cuts decided from the block total");
+    expect(flagged > 0, "nucleus: cuts within the slack flagged");
+}
+
 } // namespace
 
 int main()
 {
+    nucleus_checks();
+
     const Shape shapes[] = {{256, 2048, NUT_INT4}, {256, 2048, NUT_INT8}, {300, 96, NUT_INT4},
                             {7, 4096, NUT_INT8}, {1, 33, NUT_INT4}, {5632, 64, NUT_INT4}};
     constexpr int kCallers = 4;

@@ -7,8 +7,9 @@ paths run the same arithmetic, so they are expected to agree bit for bit.
 
 Two calls in a row, the second with a smaller input (a shorter context,
 then a smaller model), so the second call finds the first call's scratch
-contents; plus the limits: bad tokens fail as nut_decode does, a model
-the step kernels cannot run is rejected.
+contents; every call leaves the library's count of device allocations
+(nut_device_allocations) unchanged; plus the limits: bad tokens fail as
+nut_decode does, a model the step kernels cannot run is rejected.
 """
 import numpy as np
 import pytest
@@ -35,7 +36,11 @@ def run_pair(gpu, dev, c, prompt, tokens, out):
     dev.prefill(cb, prompt)
     for i, token in enumerate(tokens):
         ha = dev.decode(ca, token)
+        before = gpu.device_allocations()
         dev.decode_noalloc(cb, token, out)
+        made = gpu.device_allocations() - before
+        print(f"nut_decode_noalloc made {made} device allocations", flush=True)
+        assert made == 0
         hb = out.download(np.float32, c.dim)
         err = rel_l2(hb, ha)
         print(f"context {len(prompt) + i}: hidden rel-L2 {err:.2e}, "
