@@ -299,8 +299,10 @@ int nut_model_set_path(nut_model *m, int path);
 /* Phase timeline of the cooperative token kernel, for profiling (no
  * reference counterpart). mode 0 records nothing, 1 workgroup 0, 2 every
  * workgroup of the grid (256): each stamps the device's constant 100 MHz
- * clock at each phase boundary; per decode iteration 2 + 13 * layers
- * entries: iteration start, token known, then per layer the times its QKV
+ * clock at each phase boundary; per decode iteration 4 + 13 * layers
+ * entries: iteration start, classifier input staged, classifier pass done,
+ * token known (the generate loop; zero in the prefill loop), then per
+ * layer the times its QKV
  * input is staged, QKV published, Wo/K/V DMA issued, attention input
  * staged, attention done, Wo published, gate/up DMA issued, FFN input
  * staged, gate/up published, down DMA issued, down input staged, down

@@ -519,9 +519,9 @@ class DeviceModel:
 
     def timeline(self, iterations):
         """Phase timeline of the last token-kernel launch, in microseconds
-        from workgroup 0's first mark: array [iterations, 2 + 13 * layers],
+        from workgroup 0's first mark: array [iterations, 4 + 13 * layers],
         or [workgroups, iterations, marks] when every workgroup records."""
-        marks = 2 + 13 * self.config.layers
+        marks = 4 + 13 * self.config.layers
         wgs = getattr(self, "_timeline_wgs", 1)
         per = self.config.max_seq * marks
         out = np.zeros(max(wgs, 1) * per, np.uint64)

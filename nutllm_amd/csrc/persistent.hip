@@ -363,24 +363,16 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         return reinterpret_cast<const uint16_t *>(
             a.weights + size_t(layer) * G::LAY.bytes + G::LAY.scales[m]);
     };
-    // matrix m of layer `layer` stays in the memory-side cache (default
-    // policy) instead of streaming (non-temporal)
-    auto resident = [&](int layer, int m) {
-        return layer < a.resident_layers && ((a.resident_mask >> m) & 1) != 0;
-    };
     auto stage = [&](uint8_t *region, int rows, int rb, int sb, int layer,
                      int m, int lo, int hi, int first) {
         if (hi <= lo)
             return;
-        const uint8_t *d = wdata(layer, m) + size_t(lo) * rb;
-        const uint8_t *sc = reinterpret_cast<const uint8_t *>(wscales(layer, m)) + size_t(lo) * sb;
-        if (resident(layer, m)) {
-            dma<0>(region + first * rb, d, (hi - lo) * rb);
-            dma<0>(region + rows * rb + first * sb, sc, (hi - lo) * sb);
-        } else {
-            dma(region + first * rb, d, (hi - lo) * rb);
-            dma(region + rows * rb + first * sb, sc, (hi - lo) * sb);
-        }
+        dma(region + first * rb, wdata(layer, m) + size_t(lo) * rb,
+            (hi - lo) * rb);
+        dma(region + rows * rb + first * sb,
+            reinterpret_cast<const uint8_t *>(wscales(layer, m)) +
+                size_t(lo) * sb,
+            (hi - lo) * sb);
     };
     // The group's rows [lo, hi) are q rows of its heads, then its k and v
     // rows.
@@ -479,22 +471,27 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     xcls[i] = h_raw[i] * scale * nw.v[u];
             }
             __syncthreads();
+            mark(it, 1);
             float best_v;
             int best_i;
             if (a.classifier8 != nullptr) {
                 screen_x_digits<G::DIM>(xcls, xl, xsc, qkv);
-                classifier_screened<G::DIM>(wcls, a.classifier8, a.classifier8_scales, xcls, xl,
+                classifier_screened<G::DIM, false, 4, 3>(wcls, a.classifier8, a.classifier8_scales,
+                                                         xcls, xl,
                                             xsc, qkv, a.vocab, scores, red, best_v, best_i);
             } else {
                 classifier_best<G::DIM>(wcls, xcls, a.vocab, best_v, best_i);
             }
             __syncthreads();
+            mark(it, 2);
             // Layer 0's QKV rows stream into LDS during the argmax exchange.
             stage_qkv(0);
-            const int bi = argmax_exchange(a.x_part, best_v, best_i, red, misc, tag, error);
+            bool failed_wait = false;
+            const int bi =
+                argmax_exchange(a.x_part, best_v, best_i, red, misc, tag, error, failed_wait);
             tag++;
             token = (bi >= 0 && bi < a.vocab) ? bi : 0;
-            if (wg_failed(error, misc + 8))
+            if (failed_wait)
                 break;
             if (token == a.eos) {
                 done = 1;
@@ -509,7 +506,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
         }
         last_token = token;
         const int pos = a.start_len + it;
-        mark(it, 1);
+        mark(it, 3);
 
         for (int l = 0; l < a.layer_count; l++) {
             float *kc = a.k_cache + l * kv_layer;
@@ -550,7 +547,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                                                                    error);
             }
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
-            mark(it, 2 + 13 * l);
+            mark(it, 4 + 13 * l);
             {
                 XDigits<G::CPL_DIM> x;
                 load_x(x, xl, xsc, G::BLK_DIM);
@@ -586,7 +583,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // K/V rows of earlier positions stream into LDS while the q/k/v
             // exchange completes.
             __syncthreads();
-            mark(it, 3 + 13 * l);
+            mark(it, 5 + 13 * l);
             const int n = pos + 1;
             // LONG: this workgroup's attention unit is KV head ag over
             // positions [ap0, ap1), K rows at kst and V rows at vst
@@ -611,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 dma_padded_rows<kAgentCoherent>(vst, vc + size_t(grp) * a.max_seq * G::HD, pos);
             }
             stage_wo(l);
-            mark(it, 4 + 13 * l);
+            mark(it, 6 + 13 * l);
 
             // ---------------------------- phase B: attention + Wo + residual --
             // (take also completes the phase-A K/V stores of this wave before
@@ -634,7 +631,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
 
             __syncthreads();
-            mark(it, 5 + 13 * l);
+            mark(it, 7 + 13 * l);
             if constexpr (LONG) {
                 split_attention<G>(ap1 - ap0, ag, kst, vst, qkv, scores, xs, a, xo + ON_WO,
                                    tag, error);
@@ -693,7 +690,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                                           threadIdx.x >> 3, threadIdx.x & 7, xl, xsc);
             }
             __syncthreads();
-            mark(it, 6 + 13 * l);
+            mark(it, 8 + 13 * l);
             if constexpr (LONG) {
                 for (int r = wave; r < wo_e - wo_b; r += kWaves) {
                     const uint8_t *d;
@@ -723,9 +720,9 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             // every wave is past attention (region 1) and past its reads of
             // h_raw, which phase C's take overwrites
             __syncthreads();
-            mark(it, 7 + 13 * l);
+            mark(it, 9 + 13 * l);
             stage_gu(l);
-            mark(it, 8 + 13 * l);
+            mark(it, 10 + 13 * l);
 
             // ------------------------------------------ phase C: gate/up --
             nw4 = reinterpret_cast<const float4 *>(norm(l, true))[threadIdx.x];
@@ -754,7 +751,7 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 sq = take_once_sum<G::DIM, G::KVH, PollDelay<LONG>::C>(xo + ON_WO, h_raw,
                                                                       error);
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
-            mark(it, 9 + 13 * l);
+            mark(it, 11 + 13 * l);
             {
                 XDigits<G::CPL_DIM> x;
                 load_x(x, xl, xsc, G::BLK_DIM);
@@ -772,14 +769,14 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
             tag++;
             __syncthreads();
-            mark(it, 10 + 13 * l);
+            mark(it, 12 + 13 * l);
             stage_down(l);
-            mark(it, 11 + 13 * l);
+            mark(it, 13 + 13 * l);
 
             // --------------------------------------------- phase D: down --
             take_once<G::FFN, true, PollDelay<LONG>::D>(xo + ON_GU, xs, error);
             block_sums(xs, xsc, G::FFN);
-            mark(it, 12 + 13 * l);
+            mark(it, 14 + 13 * l);
             {
                 const bool last = l + 1 == a.layer_count;
                 for (int r = wave; r < dn_e - dn_b; r += kWaves) {
@@ -795,16 +792,19 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                     }
                 }
                 __syncthreads();
-                mark(it, 13 + 13 * l);
+                mark(it, 15 + 13 * l);
                 if (!last)
                     stage_qkv(l + 1);
             }
             hidden_once = xo + ON_DN;
             slice = slice + 1 == kOnceRing ? 0 : slice + 1;
             tag++;
-            mark(it, 14 + 13 * l);
+            mark(it, 16 + 13 * l);
         }
-        if (wg_failed(error, misc + 8))
+        // The generate loop learns of a failed wait in the next argmax
+        // exchange (every wait gives up once the flag is set, so the grid
+        // drains either way); the prefill loop checks here.
+        if (!CLASSIFY && wg_failed(error, misc + 8))
             break;
     }
     // hidden_out after an early stop (eos): the state the loop ended with

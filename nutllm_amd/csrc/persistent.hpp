@@ -53,12 +53,6 @@ struct TokenArgs {
     // timeline_cap entries per workgroup.
     unsigned long long *timeline;
     int timeline_cap, timeline_wgs;
-    // Weight rows of matrix m (bit m: q, k, v, o, gate, up, down) of layers
-    // below resident_layers are staged with the default cache policy, so
-    // they stay in the memory-side cache from token to token; the rest
-    // stream (non-temporal).
-    int resident_layers;
-    unsigned resident_mask;
     int layer_count, vocab, max_seq, eos;
     int start_len, n_iter, classify;
     float attn_scale;
@@ -134,13 +128,14 @@ inline long long token_tags_needed(long long n_iter, long long layers)
     return n_iter * (1 + 6 * layers) + 1;
 }
 
-// Timeline entries per iteration: iteration start, token known, then per
+// Timeline entries per iteration: iteration start, classifier input staged,
+// classifier pass done (this workgroup's best row), token known, then per
 // layer, for each of the phases A, B, C, D: input staged, outputs published
 // (every wave past its publishes), next weights issued to LDS DMA; phase B
 // also marks attention done after its input.
 __host__ __device__ inline int marks_per_iteration(int layers)
 {
-    return 2 + 13 * layers;
+    return 4 + 13 * layers;
 }
 
 // Longest context (positions) the kernel's fused attention phase handles

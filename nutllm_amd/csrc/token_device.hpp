@@ -96,26 +96,6 @@ __device__ __forceinline__ bool wg_failed(const int *error, int *slot)
     return *slot != 0;
 }
 
-// Re-poll *p until its tag matches (bounded; gives up once any wait failed).
-__device__ __noinline__ uint64_t wait_tag(const uint64_t *p, unsigned tag,
-                                          int *error)
-{
-    uint64_t v = load_coherent(p);
-    int spins = 0;
-    while (unsigned(v >> 32) != tag) {
-        __builtin_amdgcn_s_sleep(2);
-        v = load_coherent(p);
-        if ((++spins & 63) == 0 && failed(error))
-            break;
-        if (spins > kSpinLimit) {
-            __hip_atomic_store(error, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-    }
-    return v;
-}
-
 __device__ __forceinline__ int wave_index()
 {
     return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -828,34 +808,45 @@ __device__ __forceinline__ void classifier_best(const float *cls, const float *x
     }
 }
 
-// The fp32 logit of classifier row `row` against x (xs, DIM floats in plain
-// order), in every lane: the arithmetic of classifier_best, so both give
-// the same value for a row.
-template <int DIM, bool FRESH = false>
-__device__ __forceinline__ float classifier_row(const float *cls, const float *xs, int row)
+// The fp32 logits of NR classifier rows against x (xs, DIM floats in plain
+// order), in every lane: every row's loads are issued before any row's dot,
+// so NR rows cost one memory round trip. Per row the arithmetic is
+// classifier_best's (lane l: float4 chunks l, l + 64, ... in order, one
+// fmaf chain, then the wave sum), so both give the same value for a row.
+template <int DIM, bool FRESH, int NR>
+__device__ __forceinline__ void classifier_rows(const float *cls, const float *xs,
+                                                const int (&row)[NR], float (&out)[NR])
 {
     const int lane = FRESH ? opaque_lane_value(threadIdx.x & (kWave - 1))
                            : int(threadIdx.x & (kWave - 1));
     constexpr int C4 = DIM / 4 / kWave;
     const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-    const float4 *w0 = reinterpret_cast<const float4 *>(cls + size_t(row) * DIM);
-    float s0 = 0.0f;
+    float4 v[NR][C4];
 #pragma unroll
-    for (int j0 = 0; j0 < C4; j0 += 4) {
-        float4 v0[4];
+    for (int r = 0; r < NR; r++) {
+        const float4 *w = reinterpret_cast<const float4 *>(cls + size_t(row[r]) * DIM);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            v0[j] = w0[lane + kWave * (j0 + j)];
+        for (int j = 0; j < C4; j++)
+            v[r][j] = w[lane + kWave * j];
+    }
+    float s[NR];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 x = x4[lane + kWave * (j0 + j)];
-            s0 = fmaf(v0[j].x, x.x, s0);
-            s0 = fmaf(v0[j].y, x.y, s0);
-            s0 = fmaf(v0[j].z, x.z, s0);
-            s0 = fmaf(v0[j].w, x.w, s0);
+    for (int r = 0; r < NR; r++)
+        s[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C4; j++) {
+        const float4 x = x4[lane + kWave * j];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            s[r] = fmaf(v[r][j].x, x.x, s[r]);
+            s[r] = fmaf(v[r][j].y, x.y, s[r]);
+            s[r] = fmaf(v[r][j].z, x.z, s[r]);
+            s[r] = fmaf(v[r][j].w, x.w, s[r]);
         }
     }
-    return wave_total(s0);
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+        out[r] = wave_total(s[r]);
 }
 
 // Rows of the workgroup's classifier share one screened argmax can track:
@@ -909,7 +900,7 @@ __host__ __device__ constexpr float screen_kappa(int n)
 // row) and fp16 block scales s_jb rounded up from max|w| / 127 (c8s). Its
 // logit a_j = sum_b s_jb xsc_b (integer block dot of q and the digits of
 // x) satisfies |s_j - a_j| <= E_j = screen_kappa(DIM) T_j, s_j the fp32
-// logit (classifier_row), widened by the fp32 rounding of a_j +- E_j. With
+// logit (classifier_rows), widened by the fp32 rounding of a_j +- E_j. With
 // L = max_j (a_j - E_j) over the workgroup's rows and k the row attaining
 // it, every row with a_j + E_j < L has s_j <= a_j + E_j < L <= s_k, so only
 // the other rows (the candidates, k among them) need their fp32 logits:
@@ -919,8 +910,12 @@ __host__ __device__ constexpr float screen_kappa(int n)
 // upper: LDS, screened_rows(vocab) floats; red: LDS, kWaves floats. Ends
 // without a barrier: red is read until every wave has passed the candidate
 // step. ROWS: rows whose loads a wave issues together (measured: 1 to 4 the
-// same for dim 2048; 1 is 6 us per token faster than 4 for dim 4096).
-template <int DIM, bool FRESH = false, int ROWS = 4>
+// same for dim 2048; 1 is 6 us per token faster than 4 for dim 4096). CAND:
+// candidate rows whose fp32 loads a wave issues together. The candidates
+// of one workgroup number 4 at the median but up to two dozen (TinyLlama
+// INT4 bench model), and the argmax exchange waits for the workgroup with
+// the most, so their rows go in batches of CAND per wave.
+template <int DIM, bool FRESH = false, int ROWS = 4, int CAND = 1>
 __device__ void classifier_screened(const float *cls, const uint8_t *c8, const uint16_t *c8s,
                                     const float *xs, const uint32_t *xl, const float *xsc,
                                     const float *xl1, int vocab, float *upper, float *red,
@@ -990,10 +985,26 @@ __device__ void classifier_screened(const float *cls, const uint8_t *c8, const u
     for (int w = 1; w < kWaves; w++)
         bound = fmaxf(bound, red[w]);
 
-    // candidates in row order, the c-th to wave c % kWaves; exact logits
+    // candidates in row order, the c-th to wave c % kWaves; exact logits,
+    // CAND rows of a wave at a time (a short last batch repeats its first
+    // row, whose duplicate logit changes nothing)
     best_v = -INFINITY;
     best_i = 0x7fffffff;
-    int seen = 0;
+    int seen = 0, held = 0;
+    int rows[CAND];
+#pragma unroll
+    for (int r = 0; r < CAND; r++)
+        rows[r] = wb;
+    auto flush = [&]() {
+        float v[CAND];
+        classifier_rows<DIM, FRESH, CAND>(cls, xs, rows, v);
+#pragma unroll
+        for (int r = 0; r < CAND; r++)
+            if (v[r] > best_v || (v[r] == best_v && rows[r] < best_i)) {
+                best_v = v[r];
+                best_i = rows[r];
+            }
+    };
     for (int base = 0; base < we - wb; base += kWave) {
         const int i = base + lane;
         const bool cand = i < we - wb && !(upper[i] < bound);
@@ -1003,24 +1014,37 @@ __device__ void classifier_screened(const float *cls, const uint8_t *c8, const u
             mask &= mask - 1;
             if (seen % kWaves == wave) {
                 const int row = wb + base + bit;
-                const float v = classifier_row<DIM, FRESH>(cls, xs, row);
-                if (v > best_v || (v == best_v && row < best_i)) {
-                    best_v = v;
-                    best_i = row;
+#pragma unroll
+                for (int r = 0; r < CAND; r++)
+                    if (r == held)
+                        rows[r] = row;
+                if (held == 0) {
+#pragma unroll
+                    for (int r = 1; r < CAND; r++)
+                        rows[r] = row;
+                }
+                if (++held == CAND) {
+                    flush();
+                    held = 0;
                 }
             }
             seen++;
         }
     }
+    if (held > 0)
+        flush();
 }
 
 // First-index argmax over the grid from every wave's best (value, row):
 // the workgroup's best is published as two tagged words in x_part
 // (value, then index at x_part + kGrid), and every workgroup reduces all
-// kGrid partials to the same row. red, misc: LDS, kWaves entries each.
+// kGrid partials to the same row. red, misc: LDS, kWaves + 1 entries each.
+// failed: the error flag (a bounded wait timed out), read with the first
+// poll of the partials instead of in a round trip of its own, the same
+// value in every thread of the workgroup.
 __device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, int best_i,
                                                float *red, int *misc, unsigned tag,
-                                               int *error)
+                                               int *error, bool &failed_wait)
 {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = wave_index();
@@ -1044,13 +1068,27 @@ __device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, i
     // every workgroup reduces all partials to the same token
     float pv = -INFINITY;
     int pi = 0x7fffffff;
+    int err = 0;
+    if (threadIdx.x == kGrid)
+        err = failed(error) ? 1 : 0;
     if (threadIdx.x < kGrid) {
+        // both words of a partial polled together, so the pair costs one
+        // round trip once its producer has published
         uint64_t v = load_coherent(x_part + threadIdx.x);
         uint64_t i = load_coherent(x_part + kGrid + threadIdx.x);
-        if (unsigned(v >> 32) != tag)
-            v = wait_tag(x_part + threadIdx.x, tag, error);
-        if (unsigned(i >> 32) != tag)
-            i = wait_tag(x_part + kGrid + threadIdx.x, tag, error);
+        for (int spins = 0; unsigned(v >> 32) != tag || unsigned(i >> 32) != tag; spins++) {
+            if ((spins & 63) == 63 && failed(error))
+                break;
+            if (spins > kSpinLimit) {
+                __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            if (unsigned(v >> 32) != tag)
+                v = load_coherent(x_part + threadIdx.x);
+            if (unsigned(i >> 32) != tag)
+                i = load_coherent(x_part + kGrid + threadIdx.x);
+        }
         pv = __uint_as_float(unsigned(v));
         pi = int(unsigned(i));
     }
@@ -1068,6 +1106,8 @@ __device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, i
         red[wave] = pv;
         misc[wave] = pi;
     }
+    if (threadIdx.x == kGrid)
+        misc[kWaves] = err;
     __syncthreads();
     float bv = red[0];
     int bi = misc[0];
@@ -1076,6 +1116,7 @@ __device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, i
             bv = red[w];
             bi = misc[w];
         }
+    failed_wait = misc[kWaves] != 0;
     return bi;
 }
 

@@ -518,6 +518,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                     xcls[i] = hbuf[i] * scale * fw.v[u];
             }
             __syncthreads();
+            mark(it, 1);
             float best_v;
             int best_i;
             if (a.classifier8 != nullptr) {
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 // ST_GU after x
                 float *xl1 = xcls + G::DIM, *upper = xl1 + G::BLK_DIM;
                 screen_x_digits<G::DIM>(xcls, xl, xsc, xl1);
-                classifier_screened<G::DIM, true, 1>(fresh(a.classifier), fresh(a.classifier8),
+                classifier_screened<G::DIM, true, 1, 2>(fresh(a.classifier), fresh(a.classifier8),
                                                   fresh(a.classifier8_scales), xcls, xl, xsc,
                                                   xl1, a.vocab, upper, red, best_v, best_i);
             } else {
@@ -534,12 +535,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             }
             // every wave is past its reads of x before the q/k rows land
             __syncthreads();
+            mark(it, 2);
             // layer 0's inputs stream during the argmax exchange
             issue_a(0);
-            const int bi = argmax_exchange(fresh(a.x_part), best_v, best_i, red, misc, tag, error);
+            bool failed_wait = false;
+            const int bi = argmax_exchange(fresh(a.x_part), best_v, best_i, red, misc, tag, error,
+                                           failed_wait);
             tag++;
             token = (bi >= 0 && bi < a.vocab) ? bi : 0;
-            if (wg_failed(error, misc + 8))
+            if (failed_wait)
                 break;
             if (token == a.eos) {
                 done = 1;
@@ -553,7 +557,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             issue_a(0);
         }
         last_token = token;
-        mark(it, 1);
+        mark(it, 3);
 
         for (int l = 0; l < a.layer_count; l++) {
             const bool last = l + 1 == a.layer_count;
@@ -575,7 +579,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             // this wave's residual inputs
             float res0 = hbuf[ra], res1 = hbuf[rb];
             stage_quartets<G::QT, G::XQ>(hbuf, nw, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
-            mark(it, 2 + 13 * l);
+            mark(it, 4 + 13 * l);
             {
                 // wave w: q, k and v rows 2 w, 2 w + 1 of the slice
                 int code[6], scale[6];
@@ -613,7 +617,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             }
             // q/k/v of the slice are in LDS, and the q/k staging is free
             __syncthreads();
-            mark(it, 3 + 13 * l);
+            mark(it, 5 + 13 * l);
 
             // ------------------------------ phase B: attention over dims --
             // V rows and this wave's Wo rows (registers) stream during the
@@ -656,7 +660,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                     }
                 }
             }
-            mark(it, 4 + 13 * l);
+            mark(it, 6 + 13 * l);
             // scores: the group's partials summed in a fixed order
             float s[G::PPT];
             {
@@ -753,7 +757,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 put_once(once(0) + qkv0 + threadIdx.x, t / total);
             }
             tag++;
-            mark(it, 5 + 13 * l);
+            mark(it, 7 + 13 * l);
 
             // ------------------------------------ Wo rows + residual --
             take_once<G::DIM, false, kWidePollDelayContext, true>(once(0), hbuf, error);
@@ -764,7 +768,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                     ones[u] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
                 stage_quartets<G::QT, G::XQ>(hbuf, ones, 1.0f, xl, xsc);
             }
-            mark(it, 6 + 13 * l);
+            mark(it, 8 + 13 * l);
             {
                 float y[2];
                 rows_dot(wo, 2, xl, xsc, y);
@@ -776,7 +780,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 }
             }
             tag++;
-            mark(it, 7 + 13 * l);
+            mark(it, 9 + 13 * l);
 
             // ------------------------------------------ phase C: gate/up --
             // The gate/up pairs of LDS (ST_GU: gate codes, up codes, then
@@ -810,7 +814,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             }
             sq = take_once<G::DIM, false, 0, true>(once(X_WO), hbuf, error);
             stage_quartets<G::QT, G::XQ>(hbuf, nw, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
-            mark(it, 8 + 13 * l);
+            mark(it, 10 + 13 * l);
             {
                 float y[2 * G::NREG];
                 rows_dot(wr, 2 * G::NREG, xl, xsc, y);
@@ -846,7 +850,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             // every wave is past its reads of the gate/up staging, which the
             // activation overwrites
             __syncthreads();
-            mark(it, 9 + 13 * l);
+            mark(it, 11 + 13 * l);
 
             // --------------------------------------------- phase D: down --
             // this wave's W2 rows stream while the activation is exchanged
@@ -857,7 +861,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                        wscales(6, rb, G::SB_FFN));
             take_once<G::FFN, true, 0, true>(once(X_ACT), act, error);
             block_sums(act, xsc, G::FFN);
-            mark(it, 10 + 13 * l);
+            mark(it, 12 + 13 * l);
             res0 += regs_dot_floats(wd[0], act, xsc, G::BLK_FFN);
             res1 += regs_dot_floats(wd[1], act, xsc, G::BLK_FFN);
             if (lane == 0) {
@@ -872,14 +876,17 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             hidden_once = once(X_DN);
             slice = slice + 1 == kOnceRing ? 0 : slice + 1;
             tag++;
-            mark(it, 11 + 13 * l);
+            mark(it, 13 + 13 * l);
             // every wave is past its reads of the activation, which the next
             // take overwrites
             __syncthreads();
-            mark(it, 12 + 13 * l);
             mark(it, 14 + 13 * l);
+            mark(it, 16 + 13 * l);
         }
-        if (wg_failed(error, misc + 8))
+        // The generate loop learns of a failed wait in the next argmax
+        // exchange (every wait gives up once the flag is set, so the grid
+        // drains either way); the prefill loop checks here.
+        if (!CLASSIFY && wg_failed(error, misc + 8))
             break;
     }
     // hidden_out after an early stop (eos): the state the loop ended with

@@ -4,7 +4,8 @@
 
 Runs one greedy generate of the workload (default ``tinyllama_int4``) to
 warm up, then a second one with every workgroup stamping the 100 MHz
-real-time clock at 13 marks per layer (``record_timeline(2)``), and prints
+real-time clock at 4 marks per iteration and 13 per layer
+(``record_timeline(2)``), and prints
 medians over workgroups, layers and the steady iterations (the first two
 and the last are left out):
 
@@ -15,7 +16,10 @@ and the last are left out):
   workgroup holding the input (``ready``), and the publish skew (last
   publish minus median publish).
 
-Mark k of layer l is column 2 + 13 l + k of ``timeline()``: 0 A input
+Columns 0-3 of ``timeline()`` are the iteration start, the classifier's
+input staged (after the h exchange and the final rmsnorm), the classifier
+pass done and the token known (after the argmax exchange); mark k of layer
+l is column 4 + 13 l + k: 0 A input
 ready, 1 A published, 2 DMA issued, 3 B input ready, 4 attention done,
 5 B published, 6 DMA issued, 7 C input ready, 8 C published, 9 DMA
 issued, 10 D input ready, 11 D published, 12 next DMA issued.
@@ -36,6 +40,7 @@ import numpy as np
 from . import workloads
 
 MARKS = 13
+HEAD = 4  # iteration start, classifier input, classifier pass, token known
 SEGMENTS = [("A rows", 0, 1), ("A dma issue", 1, 2), ("B attention", 3, 4),
             ("B Wo rows", 4, 5), ("B dma issue", 5, 6), ("C rows", 7, 8),
             ("C dma issue", 8, 9), ("D rows", 10, 11), ("D dma issue", 11, 12)]
@@ -45,9 +50,9 @@ EXCHANGES = [("q/k/v", 1, 3, 0), ("h after Wo", 5, 7, 0), ("act", 8, 10, 0),
 
 
 def summarise(t, layers):
-    """t: [workgroups, iterations, 2 + 13 layers] in microseconds."""
+    """t: [workgroups, iterations, 4 + 13 layers] in microseconds."""
     its = range(2, t.shape[1] - 1)
-    col = lambda l, k: 2 + MARKS * l + k
+    col = lambda l, k: HEAD + MARKS * l + k
     out = {}
     for name, a, b in SEGMENTS:
         d = [t[:, it, col(l, b)] - t[:, it, col(l, a)] for it in its for l in range(layers)]
@@ -64,9 +69,25 @@ def summarise(t, layers):
     lay = [np.median(t[:, it, col(l + 1, 0)] - t[:, it, col(l, 0)])
            for it in its for l in range(layers - 1)]
     out["layer"] = float(np.median(lay))
-    out["classifier + argmax"] = float(np.median([np.median(t[:, it, 2] - t[:, it, 0])
-                                                  for it in its]))
+    classifier_parts(t, its, out)
     return out
+
+
+def classifier_parts(t, its, out):
+    """The iteration's head: the h exchange and final rmsnorm into the
+    classifier, its pass (median workgroup), the spread of the pass's end
+    (last minus median workgroup), the argmax exchange (last workgroup's
+    pass end to the median workgroup knowing the token), and all of it up
+    to layer 0's staged input."""
+    med = lambda a, b: float(np.median([np.median(t[:, it, b] - t[:, it, a])  # noqa: E731
+                                        for it in its]))
+    out["classifier input (h exchange)"] = med(0, 1)
+    out["classifier pass"] = med(1, 2)
+    out["skew classifier pass"] = float(np.mean([t[:, it, 2].max() - np.median(t[:, it, 2])
+                                                 for it in its]))
+    out["argmax exchange"] = float(np.mean([np.median(t[:, it, 3]) - t[:, it, 2].max()
+                                            for it in its]))
+    out["classifier + argmax"] = med(0, HEAD)
 
 
 WIDE_SEGMENTS = [("A issue + h exchange", -1, 0), ("A rows", 0, 1),
@@ -81,7 +102,7 @@ WIDE_SEGMENTS = [("A issue + h exchange", -1, 0), ("A rows", 0, 1),
 def summarise_wide(t, layers):
     """The wide kernel's segments: mark -1 is the previous layer's end."""
     its = range(2, t.shape[1] - 1)
-    col = lambda l, k: 2 + MARKS * l + k
+    col = lambda l, k: HEAD + MARKS * l + k
     out = {}
     for name, a, b in WIDE_SEGMENTS:
         d = []
@@ -93,8 +114,7 @@ def summarise_wide(t, layers):
     lay = [np.median(t[:, it, col(l + 1, 0)] - t[:, it, col(l, 0)])
            for it in its for l in range(layers - 1)]
     out["layer"] = float(np.median(lay))
-    out["classifier + argmax"] = float(np.median([np.median(t[:, it, 2] - t[:, it, 0])
-                                                  for it in its]))
+    classifier_parts(t, its, out)
     return out
 
 

@@ -10,21 +10,25 @@ LAYER = 17.0
 CLASSIFY = 40.0
 
 
+# the iteration's head: classifier input staged, pass done, token known
+HEAD_OFFS = [0.0, 2.5, 30.0, 38.0]
+
+
 def synthetic(wgs=8, iters=6, layers=3):
-    t = np.zeros((wgs, iters, 2 + 13 * layers))
+    t = np.zeros((wgs, iters, 4 + 13 * layers))
     for it in range(iters):
         start = it * (CLASSIFY + layers * LAYER)
         for w in range(wgs):
-            t[w, it, 0] = start
-            t[w, it, 1] = start + 1.0
+            for k, o in enumerate(HEAD_OFFS):
+                t[w, it, k] = start + o
             for l in range(layers):
                 for k, o in enumerate(OFFS):
-                    t[w, it, 2 + 13 * l + k] = start + CLASSIFY + l * LAYER + o
+                    t[w, it, 4 + 13 * l + k] = start + CLASSIFY + l * LAYER + o
             # one late publisher per publish mark: +0.4 us
             if w == wgs - 1:
                 for l in range(layers):
                     for k in (1, 5, 8, 11):
-                        t[w, it, 2 + 13 * l + k] += 0.4
+                        t[w, it, 4 + 13 * l + k] += 0.4
     return t
 
 
@@ -41,3 +45,7 @@ def test_summarise_segments_and_exchanges():
     assert np.isclose(out["skew h after Wo"], 0.4)
     assert out["layer"] == LAYER
     assert out["classifier + argmax"] == CLASSIFY
+    assert out["classifier input (h exchange)"] == HEAD_OFFS[1]
+    assert out["classifier pass"] == HEAD_OFFS[2] - HEAD_OFFS[1]
+    assert out["argmax exchange"] == HEAD_OFFS[3] - HEAD_OFFS[2]
+    assert out["skew classifier pass"] == 0.0
