@@ -323,6 +323,13 @@ int nut_model_timeline(const nut_model *m, uint64_t *ticks, size_t capacity,
  * presets a model's counter (a test hook, to cross the restart quickly). */
 int nut_token_tag_base(unsigned *launch_count, unsigned *base, int *clear);
 int nut_model_set_launch_count(nut_model *m, unsigned launch_count);
+/* Test hook of the cooperative token kernel's bounded waits (no reference
+ * counterpart): with fault = 1, workgroup 0 of every later launch leaves
+ * its words of the first step's h after W2 unpublished, so every wait for
+ * them runs into its spin limit; the launch must still end, and the call
+ * fail with NUT_EDEVICE ("token kernel: phase exchange timed out").
+ * fault = 0 restores normal launches. */
+int nut_model_inject_fault(nut_model *m, int fault);
 
 /* Device time (HIP events on the model's stream) of the decode loop of the
  * last nut_generate_greedy call: every classifier, argmax and decode step

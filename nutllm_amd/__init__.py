@@ -131,6 +131,7 @@ _SIGS = {
     "nut_model_load_llama2c": (C.c_int, [C.c_char_p, C.c_int, _P, _P]),
     "nut_model_config": (C.c_int, [_P, _P, _P, _P]),
     "nut_model_set_launch_count": (C.c_int, [_P, C.c_uint]),
+    "nut_model_inject_fault": (C.c_int, [_P, C.c_int]),
     "nut_kv_create": (C.c_int, [_P, _P]),
     "nut_kv_destroy": (C.c_int, [_P]),
     "nut_kv_length": (_SZ, [_P]),
@@ -536,6 +537,11 @@ class DeviceModel:
     def set_launch_count(self, count):
         """Preset the token kernel's launch counter (test hook)."""
         check(lib().nut_model_set_launch_count(self.handle, count))
+
+    def inject_fault(self, fault):
+        """nut_model_inject_fault: 1 makes the token kernel's waits for one
+        workgroup's words run into their spin limit (test hook)."""
+        check(lib().nut_model_inject_fault(self.handle, int(fault)))
 
     def last_decode_ms(self):
         """Device time of the last generate() decode loop (HIP events)."""

@@ -348,6 +348,15 @@ int nut_model_set_launch_count(nut_model *m, unsigned launch_count)
     });
 }
 
+int nut_model_inject_fault(nut_model *m, int fault)
+{
+    return nut::guarded([&]() {
+        nut::require(m != nullptr, NUT_EINVAL, "quantized model: null model");
+        nut::require(fault == 0 || fault == 1, NUT_EINVAL, "fault: unknown kind");
+        m->fault = fault;
+    });
+}
+
 int nut_model_load_llama2c(const char *path, int type, nut_model **out,
                            double *load_seconds)
 {

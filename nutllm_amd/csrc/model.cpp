@@ -599,6 +599,7 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
         hip_check(hipMemsetAsync(m.exchange.get(), 0,
                                  token_exchange_entries(s) * sizeof(uint64_t), m.stream),
                   "hipMemsetAsync");
+    a.fault = m.fault;
     a.layer_count = int(m.config.layers);
     a.vocab = s.vocab;
     a.max_seq = s.max_seq;
@@ -614,7 +615,9 @@ void run_token_kernel(nut_model &m, nut_kvcache &kv, size_t start, size_t n_iter
     launch_token_kernel(m.type, s, a, m.stream);
 }
 
-// After the stream synchronised: raise the kernel's bounded-wait failure.
+// After the stream synchronised: raise the kernel's bounded-wait failure,
+// once (the flag is cleared, so later calls that run no token kernel do
+// not report it again).
 void check_token_error(nut_model &m)
 {
     if (m.token_error.get() == nullptr)
@@ -622,8 +625,12 @@ void check_token_error(nut_model &m)
     int error = 0;
     hip_check(hipMemcpy(&error, m.token_error.get(), sizeof error, hipMemcpyDeviceToHost),
               "hipMemcpy");
-    if (error != 0)
+    if (error != 0) {
+        const int zero = 0;
+        hip_check(hipMemcpy(m.token_error.get(), &zero, sizeof zero, hipMemcpyHostToDevice),
+                  "hipMemcpy");
         fail(NUT_EDEVICE, "token kernel: phase exchange timed out");
+    }
 }
 
 } // namespace

@@ -87,6 +87,7 @@ struct nut_model {
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded
     int timeline_wgs = 0;        // workgroups it covers
     unsigned launch_count = 0;
+    int fault = 0; // nut_model_inject_fault
     double last_decode_device_ms = 0.0; // events around the decode loop
     std::unique_ptr<nut_kvcache> generation_cache;
 

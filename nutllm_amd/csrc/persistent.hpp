@@ -53,6 +53,9 @@ struct TokenArgs {
     // timeline_cap entries per workgroup.
     unsigned long long *timeline;
     int timeline_cap, timeline_wgs;
+    // Test hook (nut_model_inject_fault): 1 = workgroup 0 leaves its words
+    // of the first step's h after W2 unpublished.
+    int fault;
     int layer_count, vocab, max_seq, eos;
     int start_len, n_iter, classify;
     float attn_scale;

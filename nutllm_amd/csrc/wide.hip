@@ -123,6 +123,9 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // their phase's weight DMA already; 600 ns more on them cost 9 us.
 constexpr int kWidePollDelayScores = 120;
 constexpr int kWidePollDelayContext = 240;
+// The classifier's input (the last layer's h after W2): 600 ns as in the
+// TinyLlama-shape kernel (1,548.8 against 1,549.7 us per token with none).
+constexpr int kWidePollDelayClassifier = 60;
 
 // Cache policy of the weight loads: non-temporal (nt, bit 1), as each
 // weight byte is read once per token and the memory-side cache is left to
@@ -508,7 +511,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
                 sq = h.store(hbuf);
                 __syncthreads();
             } else {
-                sq = take_once<G::DIM, false, 0, true>(hidden_once, hbuf, error);
+                sq = take_once<G::DIM, false, kWidePollDelayClassifier, true>(hidden_once, hbuf,
+                                                                              error);
             }
             const float scale = rms_scale(wg_sum(sq, red), G::DIM);
 #pragma unroll

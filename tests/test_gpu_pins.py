@@ -18,10 +18,13 @@
 * QuantizedModelWeights::storage_bytes (src/quant_model.cpp:140-156) equal
   to the value the reference computed for the same model.
 * The token kernel's exchange tags across a restart of their 32-bit range.
+* The token kernel's bounded waits: a word that is never published ends
+  the launch with the error flag instead of a hang.
 """
 import dataclasses
 import json
 import os
+import time
 
 import numpy as np
 import pytest
@@ -337,4 +340,32 @@ def test_token_kernel_tags_across_restart(gpu):
             assert rel_l2(dev.decode(cache, ref_short[0]), ref_h2) <= TOL
     finally:
         dev.set_path(0)
+        dev.close()
+
+
+def test_token_kernel_bounded_waits_end_the_launch(gpu):
+    """A wait that never completes (nut_model_inject_fault: workgroup 0
+    leaves its words of the first step's h after W2 unpublished) runs into
+    its spin limit and raises the error flag; every later wait gives up once
+    it sees the flag, the generate loop leaves at its next argmax exchange,
+    the launch ends, and the call fails with DeviceError, once: the next
+    call (its prompt on the step kernels, then a token-kernel launch) gives
+    the oracle's greedy ids."""
+    O.orc().orc_set_threads(16)
+    model = W.build("tinyllama", 1, 3, 256)
+    c = model.config
+    prompt = gpu.synth_tokens(3, c.vocab_size, 5)
+    ref, _, _ = O.oracle_model(model).generate(prompt, 4)
+    dev = model.to_device()
+    try:
+        assert dev.generate(prompt, 4)[0] == ref
+        dev.inject_fault(1)
+        t0 = time.time()
+        with pytest.raises(gpu.DeviceError, match="timed out"):
+            dev.generate(prompt, 4)
+        print(f"faulted generate ended after {time.time() - t0:.2f} s", flush=True)
+        dev.inject_fault(0)
+        assert dev.generate(prompt, 4)[0] == ref
+    finally:
+        dev.inject_fault(0)
         dev.close()
