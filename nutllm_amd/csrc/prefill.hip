@@ -200,22 +200,22 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p)
         (const __attribute__((address_space(3))) char *)(p)));
 }
 
-// LDS DMA of 16 (or 4) bytes per lane to lds + 16 (or 4) * lane, written as
-// asm: the compiler then neither tracks the DMA (it would wait for all of
-// it before any LDS read, as it cannot tell the ring slots apart) nor moves
-// memory operations across it. The LDS base must be wave-uniform.
-__device__ __forceinline__ void dma16(const void *src, const void *lds)
+// LDS DMA of 16 (or 4) bytes per lane to LDS byte address m0 + 16 (or 4) *
+// lane, written as asm: the compiler then neither tracks the DMA (it would
+// wait for all of it before any LDS read, as it cannot tell the ring slots
+// apart) nor moves memory operations across it. m0 is wave-uniform (an
+// SGPR), formed once per kernel: recomputing it from a pointer at every
+// issue cost each wave-stage about 20 VALU and 30 SALU instructions.
+__device__ __forceinline__ void dma16(const void *src, uint32_t m0)
 {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(src), "s"(m0)
                  : "memory", "m0");
 }
 
-__device__ __forceinline__ void dma4(const void *src, const void *lds)
+__device__ __forceinline__ void dma4(const void *src, uint32_t m0)
 {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :
                  : "v"(src), "s"(m0)
@@ -271,7 +271,10 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const QMat w = segs.w[seg];
     float *__restrict__ c = segs.c[seg];
     const int ldc = segs.ldc[seg];
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    // the wave index as a scalar, so that every LDS address derived from it
+    // stays in SGPRs
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
     const int k = w.cols, n_count = w.rows, stages = k / FS;
     const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
@@ -313,38 +316,74 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const size_t s_step = size_t(n_count) * 4; // bytes per stage
     const char *const filler = reinterpret_cast<const char *>(x_hi);
     constexpr int W_STEP = QT == 1 ? FS / 2 : FS; // weight bytes per row and stage
-    auto issue = [&](GemmSlot<QT> &sl, int st) {
+    // LDS destinations (m0 values) of the wave's DMA, per ring slot
+    struct SlotM0 {
+        uint32_t xh0, xh1, xl0, xl1, w0, w1, sc;
+    };
+    auto slot_m0 = [&](GemmSlot<QT> &sl) {
+        SlotM0 m;
+        m.xh0 = __builtin_amdgcn_readfirstlane(lds_addr(&sl.xh[kWave * xi0]));
+        m.xh1 = __builtin_amdgcn_readfirstlane(lds_addr(&sl.xh[kWave * xi1]));
+        m.xl0 = __builtin_amdgcn_readfirstlane(lds_addr(&sl.xl[kWave * xi0]));
+        m.xl1 = __builtin_amdgcn_readfirstlane(lds_addr(&sl.xl[kWave * xi1]));
+        // INT4 weight instructions exist in waves 0-1 only (xi1 <= 3)
+        const bool w_here = QT == 0 || !scales;
+        m.w0 = w_here ? __builtin_amdgcn_readfirstlane(lds_addr(&sl.w[kWave * xi0])) : 0u;
+        m.w1 = w_here ? __builtin_amdgcn_readfirstlane(lds_addr(&sl.w[kWave * xi1])) : 0u;
+        m.sc = scales ? __builtin_amdgcn_readfirstlane(lds_addr(&sl.sc[kWave * si])) : 0u;
+        return m;
+    };
+    const SlotM0 m_slot[kStages] = {slot_m0(slot0), slot_m0(slot1), slot_m0(slot2)};
+    const uint32_t m_junk = __builtin_amdgcn_readfirstlane(lds_addr(&junk[0]));
+    auto issue = [&](int slot, int st) {
+        const SlotM0 &m = m_slot[slot];
         st = min(st, stages - 1); // past the end: reload the last stage
         const size_t xs = size_t(st) * (FS * 2), ws = size_t(st) * W_STEP;
-        dma16(xh0 + xs, &sl.xh[kWave * xi0]);
-        dma16(xh1 + xs, &sl.xh[kWave * xi1]);
-        dma16(xl0 + xs, &sl.xl[kWave * xi0]);
-        dma16(xl1 + xs, &sl.xl[kWave * xi1]);
+        dma16(xh0 + xs, m.xh0);
+        dma16(xh1 + xs, m.xh1);
+        dma16(xl0 + xs, m.xl0);
+        dma16(xl1 + xs, m.xl1);
         if (QT == 0) {
-            dma16(w0 + ws, &sl.w[kWave * xi0]);
-            dma16(w1 + ws, &sl.w[kWave * xi1]);
+            dma16(w0 + ws, m.w0);
+            dma16(w1 + ws, m.w1);
             if (scales)
-                dma4(s0 + size_t(st) * s_step, &sl.sc[kWave * si]);
+                dma4(s0 + size_t(st) * s_step, m.sc);
             else
-                dma4(filler, &junk[0]);
+                dma4(filler, m_junk);
         } else {
             if (scales) {
-                dma4(s0 + size_t(st) * s_step, &sl.sc[kWave * si]);
-                dma4(filler, &junk[0]);
+                dma4(s0 + size_t(st) * s_step, m.sc);
+                dma4(filler, m_junk);
             } else {
-                dma16(w0 + ws, &sl.w[kWave * xi0]);
-                dma16(w1 + ws, &sl.w[kWave * xi1]);
+                dma16(w0 + ws, m.w0);
+                dma16(w1 + ws, m.w1);
             }
-            dma4(filler, &junk[0]);
+            dma4(filler, m_junk);
         }
     };
 
-    floatx4 acc[4][2];
+    // acc += s D per block; the second block's D of a stage waits in pend
+    // (with its scales in psc) and is added at the start of the next stage,
+    // under that stage's LDS reads instead of after the stage's last MFMA.
+    // The order of the additions into acc is unchanged.
+    floatx4 acc[4][2], pend[4][2];
+    float psc[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 2; j++) {
             acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+            pend[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    auto add_pending = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[i][j][v] = fmaf(psc[j], pend[i][j][v], acc[i][j][v]);
+    };
     const int g = lane >> 4, li = lane & 15;
     const int n_lane = 32 * wave + li;
     // Fragment byte offsets in a slot (the swizzles depend on li only):
@@ -379,6 +418,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
 #pragma unroll
         for (int j = 0; j < 2; j++)
             sw[j] = sl.sc[n_lane + 16 * j];
+        add_pending(); // the previous stage's second block
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             half8 bq[2];
@@ -404,33 +444,44 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
                 for (int j = 0; j < 2; j++)
                     d[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                         __builtin_bit_cast(half8, xb[b][i]), bq[j], d[i][j], 0, 0, 0);
+            if (b == 1) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < 2; j++)
+                        pend[i][j] = d[i][j];
+                psc[0] = sc[0];
+                psc[1] = sc[1];
+            } else {
 #pragma unroll
-                    for (int v = 0; v < 4; v++)
-                        acc[i][j][v] = fmaf(sc[j], d[i][j][v], acc[i][j][v]);
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            acc[i][j][v] = fmaf(sc[j], d[i][j][v], acc[i][j][v]);
+            }
         }
     };
     // Stage s lives in slot s % 3. Step s: stage s landed in every wave
     // (stage s + 1 stays in flight), and every wave is done with stage
     // s - 1, whose slot takes stage s + 2.
-    auto step = [&](GemmSlot<QT> &cur, GemmSlot<QT> &free_slot, int st) {
+    auto step = [&](GemmSlot<QT> &cur, int free_slot, int st) {
         wait_dma_barrier<kDmaPerWave>();
         issue(free_slot, st + 2);
         stage_mma(cur);
     };
-    issue(slot0, 0);
-    issue(slot1, 1);
+    issue(0, 0);
+    issue(1, 1);
     for (int st = 0; st < stages; st += kStages) {
-        step(slot0, slot2, st);
+        step(slot0, 2, st);
         if (st + 1 < stages)
-            step(slot1, slot0, st + 1);
+            step(slot1, 0, st + 1);
         if (st + 2 < stages)
-            step(slot2, slot1, st + 2);
+            step(slot2, 1, st + 2);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // no DMA outlives the workgroup
+    add_pending();
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
