@@ -1,13 +1,16 @@
 // gemm.hip — fp32 C = A B on gfx950 matrix cores (matmul_threaded,
 // src/threading.cpp:163-181).
 //
-// v_mfma_f32_16x16x4f32 keeps fp32 inputs and accumulation. A workgroup of
-// four waves owns a 64x64 tile of C (32x32 when 64x64 tiles would not give
-// every CU one); each wave a quarter (2x2 or 1x1 MFMA tiles).
-//   tiled    M, N, K multiples of 64, 16-byte aligned rows: K advances 64
-//            at a time; the next slice is loaded (float4) into registers
-//            while the MFMAs run on the current one in LDS; A is stored
-//            transposed so fragment reads are bank-conflict free.
+// v_mfma_f32_16x16x4f32 keeps fp32 inputs and accumulation. Three kernels:
+//   ksplit   grids where 64x64 tiles would not give every CU one, M and N
+//            multiples of 32, K of 128, 16-byte aligned rows: a 32x32 tile
+//            per workgroup of eight waves, each wave the whole tile over
+//            an eighth of K, operands straight from L2 into registers, the
+//            eight partial tiles added in LDS in a fixed order;
+//   tiled    M, N, K multiples of 64 (or 32 x 32 tiles when the ksplit
+//            shape rules fail), 16-byte aligned rows: four waves each own a
+//            quarter of the tile; K advances 64 at a time through LDS, the
+//            next slice in flight in registers (A stored transposed);
 //   generic  any M, K, N: K advances 16 at a time, edges zero-filled.
 #include "kernels.hpp"
 #include "runtime.hpp"
@@ -204,6 +207,105 @@ __global__ __launch_bounds__(kThreads) void matmul_f32_tiled(
             }
 }
 
+// The k-split kernel: one 32 x 32 tile of C per workgroup of KW waves, wave
+// w taking the k range [w k / KW, (w + 1) k / KW) for the whole tile (2 x 2
+// MFMA tiles, four independent accumulators). Operands go from global
+// memory (L2) straight to registers through a DEPTH-deep ring of 16-wide k
+// chunks; no LDS staging or barrier inside the loop. In MFMA step s of a
+// chunk, lane group g (lanes 16 g .. 16 g + 15) supplies k = 4 g + s of
+// both operands: the k order inside a chunk is permuted identically for A
+// and B, so each lane's A values are four consecutive floats (one float4
+// load) and its B values four rows of one column. The KW partial tiles are
+// added in LDS in wave order, so the result does not depend on timing.
+constexpr int KW = 8, KDEPTH = 3;
+
+__global__ __launch_bounds__(64 * KW) void matmul_f32_ksplit(
+    const float *__restrict__ a, const float *__restrict__ b, float *__restrict__ c, int m,
+    int k, int n)
+{
+    __shared__ floatx4 red[KW][4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.y * 32, col0 = blockIdx.x * 32;
+    const int li = lane & 15, g = lane >> 4;
+    const int kw = k / KW, chunks = kw / 16;
+    const int kb = wave * kw;
+    const float *pa = a + size_t(row0 + li) * k + kb + 4 * g;
+    const float *pb = b + size_t(kb + 4 * g) * n + col0 + li;
+    float4 ra[KDEPTH][2];
+    float rb[KDEPTH][2][4];
+    auto load = [&](int slot, int q) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            ra[slot][i] = *reinterpret_cast<const float4 *>(pa + size_t(16 * i) * k + 16 * q);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const float *p = pb + size_t(16 * q + s) * n;
+            rb[slot][0][s] = p[0];
+            rb[slot][1][s] = p[16];
+        }
+    };
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < KDEPTH; d++)
+        if (d < chunks)
+            load(d, d);
+    for (int q0 = 0; q0 < chunks; q0 += KDEPTH) {
+#pragma unroll
+        for (int d = 0; d < KDEPTH; d++) {
+            if (q0 + d < chunks) { // workgroup-uniform
+                float av[2][4], bv[2][4];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    av[i][0] = ra[d][i].x;
+                    av[i][1] = ra[d][i].y;
+                    av[i][2] = ra[d][i].z;
+                    av[i][3] = ra[d][i].w;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++)
+                        bv[j][s] = rb[d][j][s];
+                if (q0 + d + KDEPTH < chunks)
+                    load(d, q0 + d + KDEPTH); // in flight during the MFMAs below
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+#pragma unroll
+                        for (int j = 0; j < 2; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                av[i][s], bv[j][s], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            red[wave][2 * i + j][lane] = acc[i][j];
+    __syncthreads();
+    // threads 0-255 add the KW partials of tile t = tid / 64, lane tid % 64
+    if (threadIdx.x < 256) {
+        const int t = threadIdx.x >> 6;
+        floatx4 sum = red[0][t][lane];
+#pragma unroll
+        for (int w = 1; w < KW; w++)
+            sum += red[w][t][lane];
+        const int i = t >> 1, j = t & 1;
+        // D layout: lane holds rows 4 (lane / 16) + v, column lane % 16
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            c[size_t(row0 + 16 * i + 4 * g + v) * n + col0 + 16 * j + li] = sum[v];
+    }
+}
+
 } // namespace
 
 void launch_matmul_f32(const float *a, const float *b, float *c, int m, int k,
@@ -212,7 +314,14 @@ void launch_matmul_f32(const float *a, const float *b, float *c, int m, int k,
     const dim3 grid((n + BN - 1) / BN, (m + BM - 1) / BM);
     const bool aligned = ((reinterpret_cast<uintptr_t>(a) |
                            reinterpret_cast<uintptr_t>(b)) & 15) == 0;
-    if (aligned && m % BM == 0 && n % BN == 0 && k % TK == 0) {
+    const bool few_tiles = size_t(m / BM) * (n / BN) < 256;
+    if (aligned && few_tiles && m % 32 == 0 && n % 32 == 0 && k % (16 * KW) == 0) {
+        // grids of 64 x 64 tiles that would leave CUs idle: 32 x 32 tiles
+        // with k split over the workgroup's waves (768^3: 17.8-18.7 us
+        // against 26-27 us for the tiled kernel below with 32 x 32 tiles)
+        hipLaunchKernelGGL(matmul_f32_ksplit, dim3(n / 32, m / 32), dim3(64 * KW), 0, stream,
+                           a, b, c, m, k, n);
+    } else if (aligned && m % BM == 0 && n % BN == 0 && k % TK == 0) {
         // 32 x 32 tiles when 64 x 64 ones would leave CUs without a tile
         if (size_t(m / BM) * (n / BN) < 256)
             hipLaunchKernelGGL((matmul_f32_tiled<32, 32, 1>), dim3(n / 32, m / 32),

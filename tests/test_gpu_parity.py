@@ -93,10 +93,12 @@ def test_matvec_f32_classifier(gpu, shape):
     assert rel_l2(y, ref) <= TOL
 
 
-# 768^3 runs 32 x 32 tiles, 1024 x 256 x 1024 64 x 64 tiles (256 of them),
-# the odd shapes the generic kernel
-@pytest.mark.parametrize("mkn", [(768, 768, 768), (1024, 256, 1024), (7, 9, 8),
-                                 (65, 33, 130)])
+# 768^3 and 224 x 640 x 96 run the k-split kernel (32 x 32 tiles, k over
+# eight waves), 256 x 320 x 256 (k not a multiple of 128) the tiled kernel
+# with 32 x 32 tiles, 1024 x 256 x 1024 64 x 64 tiles (256 of them), the
+# odd shapes the generic kernel
+@pytest.mark.parametrize("mkn", [(768, 768, 768), (224, 640, 96), (256, 320, 256),
+                                 (1024, 256, 1024), (7, 9, 8), (65, 33, 130)])
 def test_matmul_f32(gpu, mkn):
     m, k, n = mkn
     a = gpu.synth_normal(2, 300, m * k, sigma=1.0).reshape(m, k)
