@@ -625,22 +625,45 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
     };
-    for (int p0 = 0; p0 <= last; p0 += AK) {
-        __syncthreads(); // previous tile's readers are done
-        // K tile rows p0 .. p0 + 63 (16-byte pieces), V^T tile [d][p0 ..]
-        for (int e = tid; e < AK * HD / 8; e += NT) {
+    // The K tile rows p0 .. p0 + 63 and the V^T tile [d][p0 ..] in 16-byte
+    // pieces, PIECES per thread and array: the next tile's pieces are
+    // loaded into registers while the current tile is multiplied, and
+    // written to LDS at the start of the next iteration.
+    constexpr int PIECES = AK * HD / 8 / NT;
+    static_assert(PIECES * NT == AK * HD / 8, "whole pieces per thread");
+    uint4 nkh[PIECES], nkl[PIECES], nvh[PIECES], nvl[PIECES];
+    auto load_tile = [&](int p0) {
+#pragma unroll
+        for (int r = 0; r < PIECES; r++) {
+            const int e = tid + NT * r;
             const int j = e / (HD / 8), c8 = e % (HD / 8);
             const size_t at = size_t(p0 + j) * HD + 8 * c8;
-            *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgh + at);
-            *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = *reinterpret_cast<const uint4 *>(kgl + at);
+            nkh[r] = *reinterpret_cast<const uint4 *>(kgh + at);
+            nkl[r] = *reinterpret_cast<const uint4 *>(kgl + at);
+            const int d = e / (AK / 8), v8 = e % (AK / 8);
+            const size_t av = size_t(d) * t_pad + p0 + 8 * v8;
+            nvh[r] = *reinterpret_cast<const uint4 *>(vgh + av);
+            nvl[r] = *reinterpret_cast<const uint4 *>(vgl + av);
         }
-        for (int e = tid; e < HD * AK / 8; e += NT) {
-            const int d = e / (AK / 8), c8 = e % (AK / 8);
-            const size_t at = size_t(d) * t_pad + p0 + 8 * c8;
-            *reinterpret_cast<uint4 *>(&vsh[d][8 * c8]) = *reinterpret_cast<const uint4 *>(vgh + at);
-            *reinterpret_cast<uint4 *>(&vsl[d][8 * c8]) = *reinterpret_cast<const uint4 *>(vgl + at);
+    };
+    load_tile(0);
+    for (int p0 = 0; p0 <= last; p0 += AK) {
+        __syncthreads(); // previous tile's readers are done
+#pragma unroll
+        for (int r = 0; r < PIECES; r++) {
+            const int e = tid + NT * r;
+            const int j = e / (HD / 8), c8 = e % (HD / 8);
+            *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = nkh[r];
+            *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = nkl[r];
+            const int d = e / (AK / 8), v8 = e % (AK / 8);
+            *reinterpret_cast<uint4 *>(&vsh[d][8 * v8]) = nvh[r];
+            *reinterpret_cast<uint4 *>(&vsl[d][8 * v8]) = nvl[r];
         }
         __syncthreads();
+        if (p0 + AK <= last) // workgroup-uniform
+            load_tile(p0 + AK);
+        // keep the loads ahead of the tile's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
         // S tiles: keys 16 nt + li, rows 4 lg + v
         floatx4 sc[4];
 #pragma unroll
