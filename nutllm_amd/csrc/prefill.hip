@@ -258,12 +258,90 @@ __device__ __forceinline__ half8 codes8(uint2 raw)
     return __builtin_bit_cast(half8, make_uint4(out[0], out[1], out[2], out[3]));
 }
 
-template <int QT, bool ADD>
-__global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
+// The loader wave of qgemm_f16_kernel<QT, ADD, true>: it issues every DMA
+// instruction of a stage (x_hi and x_lo rows 8 i .. 8 i + 7, i < 8; the
+// weight rows, 16 (INT8) or 32 (INT4) per instruction; the scale dwords of
+// rows 64 i + lane, i < 2) into the three-slot ring, and meets the compute
+// waves at one barrier per stage, once stage s has landed (stage s + 1
+// stays in flight), after which stage s + 2 goes into the slot of s - 1.
+template <int QT>
+__device__ __forceinline__ void qgemm_loader(const _Float16 *x_hi, const _Float16 *x_lo,
+                                             int t_count, const QMat &w, const uint32_t *st,
+                                             int t0, int n0, GemmSlot<QT> *const (&slot)[kStages])
+{
+    constexpr int NW = QT == 1 ? 4 : 8; // weight instructions per stage
+    constexpr int D = 16 + NW + 2;      // DMA instructions per stage
+    constexpr int W_ROWS = QT == 1 ? 32 : 16;
+    constexpr int W_STEP = QT == 1 ? FS / 2 : FS;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int k = w.cols, n_count = w.rows, stages = k / FS;
+    const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
+    size_t xoff[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int row = 8 * i + (lane >> 3);
+        const int cg = (lane & 7) ^ (row & 7);
+        xoff[i] = size_t(min(t0 + row, t_count - 1)) * k + 8 * cg;
+    }
+    const char *wsrc[NW];
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        const int row = W_ROWS * i + (QT == 1 ? lane >> 1 : lane >> 2);
+        const int cg = QT == 1 ? (lane & 1) ^ ((row >> 2) & 1) : (lane & 3) ^ ((row >> 1) & 3);
+        wsrc[i] = reinterpret_cast<const char *>(w.data) +
+                  size_t(min(n0 + row, n_count - 1)) * row_bytes + 16 * cg;
+    }
+    const uint32_t *ssrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        ssrc[i] = st + min(n0 + kWave * i + lane, n_count - 1);
+    uint32_t mb[kStages];
+#pragma unroll
+    for (int r = 0; r < kStages; r++)
+        mb[r] = __builtin_amdgcn_readfirstlane(lds_addr(slot[r]));
+    auto issue = [&](int r, int s) {
+        s = min(s, stages - 1); // past the end: reload the last stage
+        const size_t xs = size_t(s) * FS, ws = size_t(s) * W_STEP;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            dma16(x_hi + xoff[i] + xs, mb[r] + offsetof(GemmSlot<QT>, xh) + 1024 * i);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            dma16(x_lo + xoff[i] + xs, mb[r] + offsetof(GemmSlot<QT>, xl) + 1024 * i);
+#pragma unroll
+        for (int i = 0; i < NW; i++)
+            dma16(wsrc[i] + ws, mb[r] + offsetof(GemmSlot<QT>, w) + 1024 * i);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            dma4(ssrc[i] + size_t(s) * n_count, mb[r] + offsetof(GemmSlot<QT>, sc) + 256 * i);
+    };
+    issue(0, 0);
+    issue(1, 1);
+    for (int s0 = 0; s0 < stages; s0 += kStages) {
+#pragma unroll
+        for (int r = 0; r < kStages; r++) {
+            if (s0 + r < stages) {
+                asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(D) : "memory");
+                issue((r + 2) % kStages, s0 + r + 2);
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // no DMA outlives the workgroup
+}
+
+// LOADER: a fifth wave issues all of a stage's DMA (qgemm_loader) and the
+// four compute waves issue none. For grids of at most one workgroup per CU
+// (the 7B shape's Wo and W2 at 512 tokens: 256 workgroups), where no second
+// workgroup runs while a wave stalls on its own DMA issue: Wo 58.0 ->
+// 53.1 us, W2 144-147 -> 130-134 us (alternated on one box). With two
+// workgroups per CU it is slower (TinyLlama gate/up at 2,048 tokens: 256 ->
+// 292 us).
+template <int QT, bool ADD, bool LOADER>
+__global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f16_kernel(
     const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
     GemmSegs segs)
 {
-    __shared__ GemmSlot<QT> slot0, slot1, slot2;
+    __shared__ GemmSlot<QT> slot[kStages];
     __shared__ uint32_t junk[kWave];
     int seg = 0, tile = blockIdx.x;
     while (seg + 1 < segs.count && tile >= segs.tiles[seg])
@@ -278,6 +356,13 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
     const int k = w.cols, n_count = w.rows, stages = k / FS;
     const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
+    if constexpr (LOADER) {
+        if (wave == kThreads / kWave) {
+            GemmSlot<QT> *const slots[kStages] = {&slot[0], &slot[1], &slot[2]};
+            qgemm_loader<QT>(x_hi, x_lo, t_count, w, segs.st[seg], t0, n0, slots);
+            return;
+        }
+    }
 
     // The wave's seven DMA instructions of a stage (every wave issues
     // seven, so one vmcnt value covers every wave): x_hi and x_lo
@@ -333,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
         m.sc = scales ? __builtin_amdgcn_readfirstlane(lds_addr(&sl.sc[kWave * si])) : 0u;
         return m;
     };
-    const SlotM0 m_slot[kStages] = {slot_m0(slot0), slot_m0(slot1), slot_m0(slot2)};
+    const SlotM0 m_slot[kStages] = {slot_m0(slot[0]), slot_m0(slot[1]), slot_m0(slot[2])};
     const uint32_t m_junk = __builtin_amdgcn_readfirstlane(lds_addr(&junk[0]));
     auto issue = [&](int slot, int st) {
         const SlotM0 &m = m_slot[slot];
@@ -466,19 +551,25 @@ __global__ __launch_bounds__(kThreads) void qgemm_f16_kernel(
     // Stage s lives in slot s % 3. Step s: stage s landed in every wave
     // (stage s + 1 stays in flight), and every wave is done with stage
     // s - 1, whose slot takes stage s + 2.
+    // With LOADER the compute waves only meet the loader at the barrier.
     auto step = [&](GemmSlot<QT> &cur, int free_slot, int st) {
-        wait_dma_barrier<kDmaPerWave>();
-        issue(free_slot, st + 2);
+        if constexpr (LOADER) {
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            wait_dma_barrier<kDmaPerWave>();
+            issue(free_slot, st + 2);
+        }
         stage_mma(cur);
     };
-    issue(0, 0);
-    issue(1, 1);
+    if constexpr (!LOADER) {
+        issue(0, 0);
+        issue(1, 1);
+    }
     for (int st = 0; st < stages; st += kStages) {
-        step(slot0, 2, st);
-        if (st + 1 < stages)
-            step(slot1, 0, st + 1);
-        if (st + 2 < stages)
-            step(slot2, 1, st + 2);
+#pragma unroll
+        for (int r = 0; r < kStages; r++)
+            if (st + r < stages) // workgroup-uniform
+                step(slot[r], (r + 2) % kStages, st + r);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // no DMA outlives the workgroup
     add_pending();
@@ -505,12 +596,21 @@ void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
     for (int i = 0; i < segs.count; i++)
         tiles += segs.tiles[i];
     const dim3 grid(tiles, (t_count + FM_ROWS - 1) / FM_ROWS);
-    if (add)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true>), grid, dim3(kThreads), 0, stream,
-                           x_hi, x_lo, t_count, segs);
+    // at most one workgroup per CU (MI355X: 256 CUs): the loader-wave form
+    const bool loader = size_t(grid.x) * grid.y <= 256;
+    const dim3 block(loader ? kThreads + kWave : kThreads);
+    if (loader && add)
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true, true>), grid, block, 0, stream, x_hi,
+                           x_lo, t_count, segs);
+    else if (loader)
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false, true>), grid, block, 0, stream, x_hi,
+                           x_lo, t_count, segs);
+    else if (add)
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true, false>), grid, block, 0, stream, x_hi,
+                           x_lo, t_count, segs);
     else
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false>), grid, dim3(kThreads), 0, stream,
-                           x_hi, x_lo, t_count, segs);
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false, false>), grid, block, 0, stream, x_hi,
+                           x_lo, t_count, segs);
 }
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
