@@ -7,8 +7,9 @@
 //   -> W2 GEMM (+ residual)
 // The quantised GEMMs run on f16 MFMA with the weight codes exact in f16,
 // the activations split into two f16 limbs and the block scales applied
-// in fp32 per 32-wide block; attention runs on fp32 MFMA. The hidden state
-// stays within about 1e-5 of the per-token path (fp32 throughout).
+// in fp32 per 32-wide block; attention runs on f16 MFMA with its operands
+// as f16 limbs, three products per term. The hidden state stays within
+// about 1e-5 of the per-token path (fp32 throughout).
 #include "prefill.hpp"
 #include "runtime.hpp"
 
@@ -113,12 +114,12 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
 //   * every product of two f16 values is exact in the fp32 accumulator;
 //   * per block, D = A_hi B + A_lo B, then acc += s_n D with the block's
 //     fp16 scale s_n (one column n per lane in the D layout).
-// A workgroup owns FM tokens x 128 outputs; four waves of (FM / 32) x 4
-// MFMA tiles. Per 32-wide k slice the limbs of X and the W
-// codes go to LDS (double-buffered) while the next three slices load into
-// registers. Lane layout (measured): A[i][k] in lane i % 16 + 16 g
-// holding k = 8 g .. 8 g + 7; B[k][n] likewise with n = lane % 16;
-// D[i][n] in lane n + 16 (i / 4), element i % 4.
+// A workgroup owns 64 tokens x 128 outputs; its four compute waves each
+// multiply all 64 tokens by 32 outputs, and the operands of each 64-wide k
+// stage reach LDS by DMA into a three-slot ring (qgemm_f16_kernel below).
+// Lane layout (measured): A[i][k] in lane i % 16 + 16 g holding
+// k = 8 g .. 8 g + 7; B[k][n] likewise with n = lane % 16; D[i][n] in
+// lane n + 16 (i / 4), element i % 4.
 constexpr int FM_ROWS = 64, FN = 128, FK = 32;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
