@@ -107,6 +107,9 @@ def test_matmul_f32(gpu, mkn):
     ref = np.empty((m, n), np.float32)
     O.orc().orc_matmul(O.ptr(a), O.ptr(b), O.ptr(ref), m, k, n)
     assert rel_l2(c, ref) <= TOL
+    # every kernel adds in a fixed order (the k-split one its eight partial
+    # tiles in wave order): a second call gives the same bits
+    assert np.array_equal(gpu.matmul_f32(a, b), c)
 
 
 @pytest.fixture(scope="module")
