@@ -494,11 +494,13 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             }
             __syncthreads();
             mark(it, 2);
-            // Layer 0's QKV rows stream into LDS during the argmax exchange.
+            // The partial leaves before layer 0's QKV rows are issued (the
+            // grid waits for the last workgroup's publish); the rows stream
+            // into LDS during the argmax exchange.
+            argmax_publish(a.x_part, best_v, best_i, red, misc, tag);
             stage_qkv(0);
             bool failed_wait = false;
-            const int bi =
-                argmax_exchange(a.x_part, best_v, best_i, red, misc, tag, error, failed_wait);
+            const int bi = argmax_take(a.x_part, red, misc, tag, error, failed_wait);
             tag++;
             token = (bi >= 0 && bi < a.vocab) ? bi : 0;
             if (failed_wait)

@@ -727,9 +727,13 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
     };
     // The K tile rows p0 .. p0 + 63 and the V^T tile [d][p0 ..] in 16-byte
-    // pieces, PIECES per thread and array: the next tile's pieces are
-    // loaded into registers while the current tile is multiplied, and
-    // written to LDS at the start of the next iteration.
+    // pieces, PIECES per thread and array. At head_dim 64 the next tile's
+    // pieces are loaded into registers while the current tile is multiplied
+    // and written to LDS at the start of the next iteration (2,048 tokens:
+    // 118.7 -> 115.0 us per layer); at head_dim 128 that costs more than it
+    // hides (512 tokens: 43.1 -> 53.0 us), so the tile is copied when it is
+    // needed.
+    constexpr bool PREFETCH = HD == 64;
     constexpr int PIECES = AK * HD / 8 / NT;
     static_assert(PIECES * NT == AK * HD / 8, "whole pieces per thread");
     uint4 nkh[PIECES], nkl[PIECES], nvh[PIECES], nvl[PIECES];
@@ -747,24 +751,46 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
             nvl[r] = *reinterpret_cast<const uint4 *>(vgl + av);
         }
     };
-    load_tile(0);
+    if constexpr (PREFETCH)
+        load_tile(0);
     for (int p0 = 0; p0 <= last; p0 += AK) {
         __syncthreads(); // previous tile's readers are done
+        if constexpr (PREFETCH) {
 #pragma unroll
-        for (int r = 0; r < PIECES; r++) {
-            const int e = tid + NT * r;
-            const int j = e / (HD / 8), c8 = e % (HD / 8);
-            *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = nkh[r];
-            *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = nkl[r];
-            const int d = e / (AK / 8), v8 = e % (AK / 8);
-            *reinterpret_cast<uint4 *>(&vsh[d][8 * v8]) = nvh[r];
-            *reinterpret_cast<uint4 *>(&vsl[d][8 * v8]) = nvl[r];
+            for (int r = 0; r < PIECES; r++) {
+                const int e = tid + NT * r;
+                const int j = e / (HD / 8), c8 = e % (HD / 8);
+                *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = nkh[r];
+                *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = nkl[r];
+                const int d = e / (AK / 8), v8 = e % (AK / 8);
+                *reinterpret_cast<uint4 *>(&vsh[d][8 * v8]) = nvh[r];
+                *reinterpret_cast<uint4 *>(&vsl[d][8 * v8]) = nvl[r];
+            }
+        } else {
+            for (int e = tid; e < AK * HD / 8; e += NT) {
+                const int j = e / (HD / 8), c8 = e % (HD / 8);
+                const size_t at = size_t(p0 + j) * HD + 8 * c8;
+                *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) =
+                    *reinterpret_cast<const uint4 *>(kgh + at);
+                *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) =
+                    *reinterpret_cast<const uint4 *>(kgl + at);
+            }
+            for (int e = tid; e < HD * AK / 8; e += NT) {
+                const int d = e / (AK / 8), c8 = e % (AK / 8);
+                const size_t at = size_t(d) * t_pad + p0 + 8 * c8;
+                *reinterpret_cast<uint4 *>(&vsh[d][8 * c8]) =
+                    *reinterpret_cast<const uint4 *>(vgh + at);
+                *reinterpret_cast<uint4 *>(&vsl[d][8 * c8]) =
+                    *reinterpret_cast<const uint4 *>(vgl + at);
+            }
         }
         __syncthreads();
-        if (p0 + AK <= last) // workgroup-uniform
-            load_tile(p0 + AK);
-        // keep the loads ahead of the tile's MFMAs
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PREFETCH) {
+            if (p0 + AK <= last) // workgroup-uniform
+                load_tile(p0 + AK);
+            // keep the loads ahead of the tile's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // S tiles: keys 16 nt + li, rows 4 lg + v
         floatx4 sc[4];
 #pragma unroll

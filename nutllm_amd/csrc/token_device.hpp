@@ -1035,16 +1035,17 @@ __device__ void classifier_screened(const float *cls, const uint8_t *c8, const u
         flush();
 }
 
-// First-index argmax over the grid from every wave's best (value, row):
-// the workgroup's best is published as two tagged words in x_part
-// (value, then index at x_part + kGrid), and every workgroup reduces all
-// kGrid partials to the same row. red, misc: LDS, kWaves + 1 entries each.
-// failed: the error flag (a bounded wait timed out), read with the first
-// poll of the partials instead of in a round trip of its own, the same
-// value in every thread of the workgroup.
-__device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, int best_i,
-                                               float *red, int *misc, unsigned tag,
-                                               int *error, bool &failed_wait)
+// First-index argmax over the grid from every wave's best (value, row), in
+// two calls: argmax_publish puts the workgroup's best as two tagged words
+// in x_part (value, then index at x_part + kGrid) and ends on a barrier, so
+// that the stores leave before any DMA the caller issues next (the grid
+// waits for the last workgroup's publish); argmax_take reduces all kGrid
+// partials to the same row in every workgroup. red, misc: LDS, kWaves + 1
+// entries each. failed: the error flag (a bounded wait timed out), read
+// with the first poll of the partials instead of in a round trip of its
+// own, the same value in every thread of the workgroup.
+__device__ __forceinline__ void argmax_publish(uint64_t *x_part, float best_v, int best_i,
+                                               float *red, int *misc, unsigned tag)
 {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = wave_index();
@@ -1065,6 +1066,14 @@ __device__ __forceinline__ int argmax_exchange(uint64_t *x_part, float best_v, i
         put(x_part + blockIdx.x, bv, tag);
         put(x_part + kGrid + blockIdx.x, __int_as_float(bi), tag);
     }
+    __syncthreads(); // red and misc are read again by argmax_take
+}
+
+__device__ __forceinline__ int argmax_take(const uint64_t *x_part, float *red, int *misc,
+                                           unsigned tag, int *error, bool &failed_wait)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = wave_index();
     // every workgroup reduces all partials to the same token
     float pv = -INFINITY;
     int pi = 0x7fffffff;

@@ -540,11 +540,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_kernel(TokenArgs a)
             // every wave is past its reads of x before the q/k rows land
             __syncthreads();
             mark(it, 2);
-            // layer 0's inputs stream during the argmax exchange
+            // the partial leaves first; layer 0's inputs then stream during
+            // the argmax exchange
+            argmax_publish(fresh(a.x_part), best_v, best_i, red, misc, tag);
             issue_a(0);
             bool failed_wait = false;
-            const int bi = argmax_exchange(fresh(a.x_part), best_v, best_i, red, misc, tag, error,
-                                           failed_wait);
+            const int bi = argmax_take(fresh(a.x_part), red, misc, tag, error, failed_wait);
             tag++;
             token = (bi >= 0 && bi < a.vocab) ? bi : 0;
             if (failed_wait)
