@@ -34,29 +34,98 @@ __global__ __launch_bounds__(kThreads) void embed_rows_kernel(
 // out[t] = h[t] * (1 / sqrt(mean(h[t]^2) + 1e-5)) * w  (src/ops.cpp:111-134)
 // An activation the GEMMs read as two f16 limbs: hi = f16(v), lo =
 // f16(v - hi), so hi + lo carries v to about 2^-22 relative.
+// v as an fp32 value in a register, opaque to the optimiser: otherwise the
+// multiply that produced v may be folded into either conversion (fma_mix
+// from the unrounded product) but not the other, and hi + lo then misses v
+// by an f16 ulp where the two roundings part (measured: rel-L2 5e-5 on the
+// K/V rows of a batched prefill instead of 5e-7).
+__device__ __forceinline__ float settle(float v)
+{
+    asm("" : "+v"(v));
+    return v;
+}
+
 __device__ __forceinline__ void put_limbs(_Float16 *hi, _Float16 *lo, size_t i, float v)
 {
+    v = settle(v);
     const _Float16 a = (_Float16)v;
     hi[i] = a;
     lo[i] = (_Float16)(v - (float)a);
 }
 
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// put_limbs of four consecutive values, i a multiple of 4: one 8-byte store
+// per limb.
+__device__ __forceinline__ void put_limbs4(_Float16 *hi, _Float16 *lo, size_t i, float4 v)
+{
+    v = make_float4(settle(v.x), settle(v.y), settle(v.z), settle(v.w));
+    half4v a, b;
+    a.x = (_Float16)v.x;
+    a.y = (_Float16)v.y;
+    a.z = (_Float16)v.z;
+    a.w = (_Float16)v.w;
+    b.x = (_Float16)(v.x - (float)a.x);
+    b.y = (_Float16)(v.y - (float)a.y);
+    b.z = (_Float16)(v.z - (float)a.z);
+    b.w = (_Float16)(v.w - (float)a.w);
+    *reinterpret_cast<half4v *>(hi + i) = a;
+    *reinterpret_cast<half4v *>(lo + i) = b;
+}
+
+// float4s of a row each thread keeps in registers between the sum of
+// squares and the scaling: rows up to 4,096 wide are read from memory once
+// (wider rows read their remainder twice).
+constexpr int kRowVecs = 4;
+
+// One workgroup per token row; dim % 4 == 0.
 __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
     const float *h, const float *w, _Float16 *out_hi, _Float16 *out_lo, int dim)
 {
     __shared__ float red[kThreads / kWave];
-    const float *x = h + size_t(blockIdx.x) * dim;
+    const float4 *x = reinterpret_cast<const float4 *>(h + size_t(blockIdx.x) * dim);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    const int n4 = dim / 4;
+    float4 v[kRowVecs];
     float sq = 0.0f;
-    for (int i = threadIdx.x; i < dim; i += kThreads)
-        sq = fmaf(x[i], x[i], sq);
+#pragma unroll
+    for (int j = 0; j < kRowVecs; j++) {
+        const int i = threadIdx.x + kThreads * j;
+        v[j] = i < n4 ? x[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < kRowVecs; j++) {
+        sq = fmaf(v[j].x, v[j].x, sq);
+        sq = fmaf(v[j].y, v[j].y, sq);
+        sq = fmaf(v[j].z, v[j].z, sq);
+        sq = fmaf(v[j].w, v[j].w, sq);
+    }
+    for (int i = threadIdx.x + kThreads * kRowVecs; i < n4; i += kThreads) {
+        const float4 u = x[i];
+        sq = fmaf(u.x, u.x, sq);
+        sq = fmaf(u.y, u.y, sq);
+        sq = fmaf(u.z, u.z, sq);
+        sq = fmaf(u.w, u.w, sq);
+    }
     const float total = block_sum(sq, red, kThreads / kWave);
     const float scale = 1.0f / sqrtf(total / float(dim) + 1e-5f);
     const size_t row = size_t(blockIdx.x) * dim;
-    for (int i = threadIdx.x; i < dim; i += kThreads)
-        put_limbs(out_hi, out_lo, row + i, x[i] * scale * w[i]);
+    auto put = [&](int i, float4 u) {
+        const float4 g = w4[i];
+        put_limbs4(out_hi, out_lo, row + 4 * size_t(i),
+                   make_float4(u.x * scale * g.x, u.y * scale * g.y, u.z * scale * g.z,
+                               u.w * scale * g.w));
+    };
+#pragma unroll
+    for (int j = 0; j < kRowVecs; j++) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < n4)
+            put(i, v[j]);
+    }
+    for (int i = threadIdx.x + kThreads * kRowVecs; i < n4; i += kThreads)
+        put(i, x[i]);
 }
 
-// act[t][i] = silu(g[t][i]) * u[t][i]  (src/quant_model.cpp:197-198)
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *g,
                                                             const float *u,
                                                             _Float16 *act_hi,
@@ -71,7 +140,8 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *g,
 
 // RoPE on q (all heads) and k (kv heads) of token t at position start + t,
 // the rotation of the decode path (src/quant_model.cpp:26-37), then K and V
-// rows into the cache [kv_head][max_seq][head_dim] of this layer.
+// rows into the cache [kv_head][max_seq][head_dim] of this layer. Each
+// (even, odd) pair moves as one float2.
 __global__ __launch_bounds__(kThreads) void rope_store_kernel(
     float *q, const float *k, const float *v, const float2 *rope, float *k_cache,
     float *v_cache, int heads, int kv_heads, int hd, int max_seq, int start)
@@ -80,25 +150,22 @@ __global__ __launch_bounds__(kThreads) void rope_store_kernel(
     const int pos = start + t;
     const int dim = heads * hd, kvd = kv_heads * hd;
     const float2 *cs = rope + size_t(pos) * (hd / 2);
+    float2 *qr = reinterpret_cast<float2 *>(q + size_t(t) * dim);
     for (int i = threadIdx.x; i < dim / 2; i += kThreads) {
-        float *p = q + size_t(t) * dim + 2 * i;
         const float2 f = cs[i % (hd / 2)];
-        const float even = p[0], odd = p[1];
-        p[0] = fmaf(even, f.x, -(odd * f.y));
-        p[1] = fmaf(even, f.y, odd * f.x);
+        const float2 e = qr[i];
+        qr[i] = make_float2(fmaf(e.x, f.x, -(e.y * f.y)), fmaf(e.x, f.y, e.y * f.x));
     }
+    const float2 *kr = reinterpret_cast<const float2 *>(k + size_t(t) * kvd);
+    const float2 *vr = reinterpret_cast<const float2 *>(v + size_t(t) * kvd);
     for (int i = threadIdx.x; i < kvd / 2; i += kThreads) {
-        const float *p = k + size_t(t) * kvd + 2 * i;
         const float2 f = cs[i % (hd / 2)];
-        const float even = p[0], odd = p[1];
+        const float2 e = kr[i];
         const int head = (2 * i) / hd, d = (2 * i) % hd;
-        float *kc = k_cache + (size_t(head) * max_seq + pos) * hd + d;
-        kc[0] = fmaf(even, f.x, -(odd * f.y));
-        kc[1] = fmaf(even, f.y, odd * f.x);
-        const float *vp = v + size_t(t) * kvd + 2 * i;
-        float *vcp = v_cache + (size_t(head) * max_seq + pos) * hd + d;
-        vcp[0] = vp[0];
-        vcp[1] = vp[1];
+        const size_t at = (size_t(head) * max_seq + pos) * hd + d;
+        *reinterpret_cast<float2 *>(k_cache + at) =
+            make_float2(fmaf(e.x, f.x, -(e.y * f.y)), fmaf(e.x, f.y, e.y * f.x));
+        *reinterpret_cast<float2 *>(v_cache + at) = vr[i];
     }
 }
 
@@ -625,30 +692,44 @@ int kv_limb_rows(const DecodeShape &s) { return (s.max_seq + AK - 1) / AK * AK; 
 // f16(v - hi)), written once per layer for the attention below: K as
 // [kv_head][pos][HD], V transposed as [kv_head][HD][pos], positions padded
 // to a multiple of 64 with zeros (a masked key then has an exact zero
-// weight times a finite value). One workgroup per (kv head, 64 positions);
+// weight times a finite value). One workgroup per (kv head, 32 positions);
 // the V tile is transposed through LDS so that reads and writes stay
-// coalesced.
+// coalesced, four values per load and per limb store.
+constexpr int kLimbTile = 32;
+
 template <int HD>
 __global__ __launch_bounds__(kThreads) void kv_limbs_kernel(
     const float *k_cache, const float *v_cache, int max_seq, int t_count, int t_pad,
     _Float16 *k_hi, _Float16 *k_lo, _Float16 *vt_hi, _Float16 *vt_lo)
 {
-    __shared__ float tile[AK][HD + 1];
-    const int kvh = blockIdx.x, p0 = blockIdx.y * AK;
-    const float *kc = k_cache + size_t(kvh) * max_seq * HD;
-    const float *vc = v_cache + size_t(kvh) * max_seq * HD;
-    for (int e = threadIdx.x; e < AK * HD; e += kThreads) {
-        const int p = e / HD, d = e % HD;
+    constexpr int P = kLimbTile, Q = HD / 4; // positions; float4s per row
+    static_assert(P * Q % kThreads == 0 && HD * (P / 4) % kThreads == 0,
+                  "whole float4s per thread");
+    static_assert(AK % P == 0, "tiles cover the padded positions");
+    __shared__ __attribute__((aligned(16))) float tile[P][HD + 4];
+    const int kvh = blockIdx.x, p0 = blockIdx.y * P;
+    const float4 *kc = reinterpret_cast<const float4 *>(k_cache + size_t(kvh) * max_seq * HD);
+    const float4 *vc = reinterpret_cast<const float4 *>(v_cache + size_t(kvh) * max_seq * HD);
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < P * Q / kThreads; u++) {
+        const int e = threadIdx.x + kThreads * u;
+        const int p = e / Q, c = e % Q;
         const bool in = p0 + p < t_count;
-        const float kv = in ? kc[size_t(p0 + p) * HD + d] : 0.0f;
-        const size_t at = (size_t(kvh) * t_pad + p0 + p) * HD + d;
-        put_limbs(k_hi, k_lo, at, kv);
-        tile[p][d] = in ? vc[size_t(p0 + p) * HD + d] : 0.0f;
+        const size_t at = size_t(min(p0 + p, t_count - 1)) * Q + c;
+        float4 kv = kc[at], vv = vc[at];
+        if (!in)
+            kv = vv = zero;
+        put_limbs4(k_hi, k_lo, (size_t(kvh) * t_pad + p0 + p) * HD + 4 * c, kv);
+        *reinterpret_cast<float4 *>(&tile[p][4 * c]) = vv;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < AK * HD; e += kThreads) {
-        const int d = e / AK, p = e % AK;
-        put_limbs(vt_hi, vt_lo, (size_t(kvh) * HD + d) * t_pad + p0 + p, tile[p][d]);
+#pragma unroll
+    for (int u = 0; u < HD * (P / 4) / kThreads; u++) {
+        const int e = threadIdx.x + kThreads * u;
+        const int d = e / (P / 4), p = 4 * (e % (P / 4));
+        put_limbs4(vt_hi, vt_lo, (size_t(kvh) * HD + d) * t_pad + p0 + p,
+                   make_float4(tile[p][d], tile[p + 1][d], tile[p + 2][d], tile[p + 3][d]));
     }
 }
 
@@ -891,6 +972,7 @@ void launch_embed_rows(const float *embeddings, const int *tokens, float *h,
 void launch_rmsnorm_rows(const float *h, const float *w, _Float16 *out_hi,
                          _Float16 *out_lo, int t_count, int dim, hipStream_t stream)
 {
+    require(dim % 4 == 0, NUT_EINVAL, "prefill rmsnorm: dim must be a multiple of 4");
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(t_count), dim3(kThreads), 0,
                        stream, h, w, out_hi, out_lo, dim);
     check_launch("prefill rmsnorm");
@@ -944,6 +1026,7 @@ void launch_rope_store(float *q, const float *k, const float *v,
                        const DecodeShape &s, int t_count, int start,
                        hipStream_t stream)
 {
+    require(s.head_dim % 2 == 0, NUT_EINVAL, "prefill rope: odd head_dim");
     hipLaunchKernelGGL(rope_store_kernel, dim3(t_count), dim3(kThreads), 0,
                        stream, q, k, v, rope, k_cache, v_cache, s.heads,
                        s.kv_heads, s.head_dim, s.max_seq, start);
@@ -964,7 +1047,7 @@ void launch_attention_prefill(const float *q, const float *k_cache,
     require(t_pad <= kv_limb_rows(s), NUT_EINVAL, "prefill attention: prompt too long");
     const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
     _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
-    const dim3 kv_grid(s.kv_heads, t_pad / AK), grid(s.heads, t_pad / AQ);
+    const dim3 kv_grid(s.kv_heads, t_pad / kLimbTile), grid(s.heads, t_pad / AQ);
     // head_dim 64: two query heads per workgroup when they share a KV head
     const bool pair = (s.heads / s.kv_heads) % 2 == 0;
     const dim3 pair_grid(s.heads / 2, t_pad / AQ);
