@@ -216,22 +216,21 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
     if (m.pf_h.get() == nullptr) {
         const size_t rows = c.max_seq;
         m.pf_h.allocate(rows * c.dim * sizeof(float));
-        m.pf_x.allocate(rows * std::max(c.dim, c.ffn_dim) * sizeof(float));
+        m.pf_x.allocate(rows * c.dim * sizeof(float));
+        m.pf_act.allocate(rows * c.ffn_dim * sizeof(float));
         m.pf_q.allocate(rows * c.dim * sizeof(float));
         m.pf_k.allocate(rows * kvd * sizeof(float));
         m.pf_v.allocate(rows * kvd * sizeof(float));
         m.pf_ctx.allocate(rows * c.dim * sizeof(float));
-        m.pf_g.allocate(rows * c.ffn_dim * sizeof(float));
-        m.pf_u.allocate(rows * c.ffn_dim * sizeof(float));
         m.pf_kv.allocate(4 * prefill_kv_limb_elems(s) * sizeof(_Float16));
     }
     const int t = int(count);
-    // GEMM inputs as f16 limbs (hi rows, then lo rows): the normalised x and
-    // the SwiGLU activations in pf_x, the attention context in pf_ctx
+    // GEMM inputs as f16 limbs (hi rows, then lo rows): the normalised x in
+    // pf_x, the attention context in pf_ctx, the SwiGLU activations in pf_act
     float *h = m.pf_h.as<float>();
     _Float16 *xh = m.pf_x.as<_Float16>(), *ch = m.pf_ctx.as<_Float16>();
+    _Float16 *act_h = m.pf_act.as<_Float16>();
     float *q = m.pf_q.as<float>(), *k = m.pf_k.as<float>(), *v = m.pf_v.as<float>();
-    float *g = m.pf_g.as<float>(), *u = m.pf_u.as<float>();
     launch_embed_rows(m.embeddings.as<float>(), m.prompt.as<int>(), h, t, s.dim,
                       m.stream);
     const size_t layer_elems = kv.layer_elements();
@@ -243,10 +242,7 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         const QMat *qkv_w[3] = {&w.query, &w.key, &w.value};
         float *const qkv_c[3] = {q, k, v};
         const int qkv_ld[3] = {s.dim, int(kvd), int(kvd)};
-        const QMat *gu_w[2] = {&w.gate, &w.up};
         const QMat *wo = &w.output, *wd = &w.down;
-        float *const gu_c[2] = {g, u};
-        const int gu_ld[2] = {s.ffn_dim, s.ffn_dim};
         launch_rmsnorm_rows(h, w.attention_norm, xh, xh + size_t(t) * s.dim, t, s.dim,
                             m.stream);
         launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, ss, qkv_c, qkv_ld, 3, false,
@@ -257,12 +253,11 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, ss + 3, &h, &s.dim, 1, true,
                           m.stream);
         launch_rmsnorm_rows(h, w.ffn_norm, xh, xh + size_t(t) * s.dim, t, s.dim, m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, gu_w, ss + 4, gu_c, gu_ld, 2, false,
-                          m.stream);
-        launch_silu_mul(g, u, xh, xh + size_t(t) * s.ffn_dim, size_t(t) * s.ffn_dim,
-                        m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.ffn_dim, t, &wd, ss + 6, &h, &s.dim, 1, true,
-                          m.stream);
+        // gate/up products and SwiGLU in one launch
+        launch_qgemm_swiglu(xh, xh + size_t(t) * s.dim, t, w.gate, w.up, ss[4], ss[5],
+                            act_h, act_h + size_t(t) * s.ffn_dim, m.stream);
+        launch_qgemm_rows(act_h, act_h + size_t(t) * s.ffn_dim, t, &wd, ss + 6, &h, &s.dim, 1,
+                          true, m.stream);
     }
     hip_check(hipMemcpyAsync(m.hidden.get(), h + size_t(t - 1) * s.dim,
                              s.dim * sizeof(float), hipMemcpyDeviceToDevice,

@@ -126,18 +126,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
         put(i, x[i]);
 }
 
-__global__ __launch_bounds__(kThreads) void silu_mul_kernel(const float *g,
-                                                            const float *u,
-                                                            _Float16 *act_hi,
-                                                            _Float16 *act_lo, size_t n)
-{
-    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i < n) {
-        const float v = g[i];
-        put_limbs(act_hi, act_lo, i, v / (1.0f + expf(-v)) * u[i]);
-    }
-}
-
 // RoPE on q (all heads) and k (kv heads) of token t at position start + t,
 // the rotation of the decode path (src/quant_model.cpp:26-37), then K and V
 // rows into the cache [kv_head][max_seq][head_dim] of this layer. Each
@@ -226,7 +214,27 @@ struct GemmSegs {
     int ldc[3];
     int tiles[3];
     int count;
+    // SwiGLU launches: w[0] gate, w[1] up; silu(gate) * up as limbs
+    _Float16 *act_hi, *act_lo;
+    int act_ld;
 };
+
+// Source row of tile row r (0 .. 127) and its matrix (0 or 1): row n0 + r
+// of the segment's matrix; for a SwiGLU tile, gate and up rows alternate in
+// groups of 16 (tile rows 32 v .. 32 v + 15 are gate rows n0 + 16 v + i,
+// tile rows 32 v + 16 .. 32 v + 31 the up rows of the same outputs), so
+// that a wave's two 16-row MFMA tiles hold gate and up of one output
+// column in the same lane.
+template <bool SWIGLU>
+__device__ __forceinline__ int tile_row_source(int r, int n0, int &mat)
+{
+    if (SWIGLU) {
+        mat = (r >> 4) & 1;
+        return n0 + 16 * (r >> 5) + (r & 15);
+    }
+    mat = 0;
+    return n0 + r;
+}
 
 // ------------------------------------------------------ quantised GEMM --
 
@@ -332,9 +340,10 @@ __device__ __forceinline__ half8 codes8(uint2 raw)
 // rows 64 i + lane, i < 2) into the three-slot ring, and meets the compute
 // waves at one barrier per stage, once stage s has landed (stage s + 1
 // stays in flight), after which stage s + 2 goes into the slot of s - 1.
-template <int QT>
+template <int QT, bool SWIGLU>
 __device__ __forceinline__ void qgemm_loader(const _Float16 *x_hi, const _Float16 *x_lo,
-                                             int t_count, const QMat &w, const uint32_t *st,
+                                             int t_count, const QMat &w, const QMat &w_up,
+                                             const uint32_t *st, const uint32_t *st_up,
                                              int t0, int n0, GemmSlot<QT> *const (&slot)[kStages])
 {
     constexpr int NW = QT == 1 ? 4 : 8; // weight instructions per stage
@@ -356,13 +365,18 @@ __device__ __forceinline__ void qgemm_loader(const _Float16 *x_hi, const _Float1
     for (int i = 0; i < NW; i++) {
         const int row = W_ROWS * i + (QT == 1 ? lane >> 1 : lane >> 2);
         const int cg = QT == 1 ? (lane & 1) ^ ((row >> 2) & 1) : (lane & 3) ^ ((row >> 1) & 3);
-        wsrc[i] = reinterpret_cast<const char *>(w.data) +
-                  size_t(min(n0 + row, n_count - 1)) * row_bytes + 16 * cg;
+        int mat;
+        const int src = tile_row_source<SWIGLU>(row, n0, mat);
+        wsrc[i] = reinterpret_cast<const char *>(mat ? w_up.data : w.data) +
+                  size_t(min(src, n_count - 1)) * row_bytes + 16 * cg;
     }
     const uint32_t *ssrc[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-        ssrc[i] = st + min(n0 + kWave * i + lane, n_count - 1);
+    for (int i = 0; i < 2; i++) {
+        int mat;
+        const int src = tile_row_source<SWIGLU>(kWave * i + lane, n0, mat);
+        ssrc[i] = (mat ? st_up : st) + min(src, n_count - 1);
+    }
     uint32_t mb[kStages];
 #pragma unroll
     for (int r = 0; r < kStages; r++)
@@ -404,11 +418,15 @@ __device__ __forceinline__ void qgemm_loader(const _Float16 *x_hi, const _Float1
 // 53.1 us, W2 144-147 -> 130-134 us (alternated on one box). With two
 // workgroups per CU it is slower (TinyLlama gate/up at 2,048 tokens: 256 ->
 // 292 us).
-template <int QT, bool ADD, bool LOADER>
+// SWIGLU: the tile holds gate and up rows of 64 outputs (tile_row_source),
+// and the epilogue writes silu(gate) * up as limbs (act_hi, act_lo) instead
+// of the two products.
+template <int QT, bool ADD, bool LOADER, bool SWIGLU>
 __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f16_kernel(
     const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
     GemmSegs segs)
 {
+    static_assert(!(ADD && SWIGLU), "one epilogue");
     __shared__ GemmSlot<QT> slot[kStages];
     __shared__ uint32_t junk[kWave];
     int seg = 0, tile = blockIdx.x;
@@ -421,13 +439,17 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
     // stays in SGPRs
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int t0 = blockIdx.y * FM_ROWS, n0 = tile * FN;
+    // first output of the tile (SWIGLU: 64 outputs, 128 rows)
+    const int t0 = blockIdx.y * FM_ROWS, n0 = tile * (SWIGLU ? FN / 2 : FN);
     const int k = w.cols, n_count = w.rows, stages = k / FS;
     const size_t row_bytes = QT == 1 ? size_t(k) / 2 : size_t(k);
+    const QMat &w_up = segs.w[SWIGLU ? 1 : 0];
+    const uint32_t *const st_up = segs.st[SWIGLU ? 1 : 0];
     if constexpr (LOADER) {
         if (wave == kThreads / kWave) {
             GemmSlot<QT> *const slots[kStages] = {&slot[0], &slot[1], &slot[2]};
-            qgemm_loader<QT>(x_hi, x_lo, t_count, w, segs.st[seg], t0, n0, slots);
+            qgemm_loader<QT, SWIGLU>(x_hi, x_lo, t_count, w, w_up, segs.st[seg], st_up, t0, n0,
+                                     slots);
             return;
         }
     }
@@ -456,16 +478,20 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
     auto w_src = [&](int i) {
         const int row = W_ROWS * i + (QT == 1 ? lane >> 1 : lane >> 2);
         const int cg = QT == 1 ? (lane & 1) ^ ((row >> 2) & 1) : (lane & 3) ^ ((row >> 1) & 3);
-        return reinterpret_cast<const char *>(w.data) +
-               size_t(min(n0 + row, n_count - 1)) * row_bytes + 16 * cg;
+        int mat;
+        const int src = tile_row_source<SWIGLU>(row, n0, mat);
+        return reinterpret_cast<const char *>(mat ? w_up.data : w.data) +
+               size_t(min(src, n_count - 1)) * row_bytes + 16 * cg;
     };
     const char *const w0 = w_src(xi0), *const w1 = w_src(xi1);
     // scale dwords of rows 64 si + lane (stage-major: consecutive rows are
     // consecutive dwords): INT8 waves 0-1, INT4 waves 2-3
     const bool scales = QT == 1 ? wave >= 2 : wave < 2; // wave-uniform
     const int si = QT == 1 ? wave - 2 : wave;
+    int s_mat;
+    const int s_row = tile_row_source<SWIGLU>(kWave * max(si, 0) + lane, n0, s_mat);
     const char *const s0 = reinterpret_cast<const char *>(
-        segs.st[seg] + min(n0 + kWave * max(si, 0) + lane, n_count - 1));
+        (s_mat ? st_up : segs.st[seg]) + min(s_row, n_count - 1));
     const size_t s_step = size_t(n_count) * 4; // bytes per stage
     const char *const filler = reinterpret_cast<const char *>(x_hi);
     constexpr int W_STEP = QT == 1 ? FS / 2 : FS; // weight bytes per row and stage
@@ -641,6 +667,23 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // no DMA outlives the workgroup
     add_pending();
+    if constexpr (SWIGLU) {
+        // acc[i][0]: gate, acc[i][1]: up of output n0 + 16 wave + li
+        // (silu as silu_mul_kernel: src/quant_model.cpp:197-200)
+        const int n = n0 + 16 * wave + li;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int t = t0 + 16 * i + 4 * g + v;
+                if (t < t_count && n < n_count) {
+                    const float gv = acc[i][0][v];
+                    put_limbs(segs.act_hi, segs.act_lo, size_t(t) * segs.act_ld + n,
+                              gv / (1.0f + expf(-gv)) * acc[i][1][v]);
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -656,29 +699,31 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
             }
 }
 
-template <int QT>
-void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
-                  const GemmSegs &segs, bool add, hipStream_t stream)
+template <int QT, bool ADD, bool SWIGLU>
+void launch_qgemm_form(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                       const GemmSegs &segs, hipStream_t stream)
 {
     int tiles = 0;
     for (int i = 0; i < segs.count; i++)
         tiles += segs.tiles[i];
     const dim3 grid(tiles, (t_count + FM_ROWS - 1) / FM_ROWS);
     // at most one workgroup per CU (MI355X: 256 CUs): the loader-wave form
-    const bool loader = size_t(grid.x) * grid.y <= 256;
-    const dim3 block(loader ? kThreads + kWave : kThreads);
-    if (loader && add)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true, true>), grid, block, 0, stream, x_hi,
-                           x_lo, t_count, segs);
-    else if (loader)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false, true>), grid, block, 0, stream, x_hi,
-                           x_lo, t_count, segs);
-    else if (add)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, true, false>), grid, block, 0, stream, x_hi,
-                           x_lo, t_count, segs);
+    if (size_t(grid.x) * grid.y <= 256)
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, true, SWIGLU>), grid,
+                           dim3(kThreads + kWave), 0, stream, x_hi, x_lo, t_count, segs);
     else
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, false, false>), grid, block, 0, stream, x_hi,
-                           x_lo, t_count, segs);
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, false, SWIGLU>), grid, dim3(kThreads), 0,
+                           stream, x_hi, x_lo, t_count, segs);
+}
+
+template <int QT>
+void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                  const GemmSegs &segs, bool add, hipStream_t stream)
+{
+    if (add)
+        launch_qgemm_form<QT, true, false>(x_hi, x_lo, t_count, segs, stream);
+    else
+        launch_qgemm_form<QT, false, false>(x_hi, x_lo, t_count, segs, stream);
 }
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
@@ -1021,6 +1066,32 @@ void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
     check_launch("prefill gemm");
 }
 
+void launch_qgemm_swiglu(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                         const QMat &gate, const QMat &up, const uint32_t *st_gate,
+                         const uint32_t *st_up, _Float16 *act_hi, _Float16 *act_lo,
+                         hipStream_t stream)
+{
+    require(gate.type == up.type && gate.cols == up.cols && gate.rows == up.rows, NUT_EINVAL,
+            "prefill gemm: gate and up differ in type or shape");
+    require(gate.cols % FS == 0 && st_gate != nullptr && st_up != nullptr, NUT_EINVAL,
+            "prefill gemm: rows of whole 64-wide stages with stage-major scales");
+    GemmSegs segs{};
+    segs.count = 1;
+    segs.w[0] = gate;
+    segs.w[1] = up;
+    segs.st[0] = st_gate;
+    segs.st[1] = st_up;
+    segs.tiles[0] = (gate.rows + FN / 2 - 1) / (FN / 2);
+    segs.act_hi = act_hi;
+    segs.act_lo = act_lo;
+    segs.act_ld = gate.rows;
+    if (gate.type == 1)
+        launch_qgemm_form<1, false, true>(x_hi, x_lo, t_count, segs, stream);
+    else
+        launch_qgemm_form<0, false, true>(x_hi, x_lo, t_count, segs, stream);
+    check_launch("prefill gemm swiglu");
+}
+
 void launch_rope_store(float *q, const float *k, const float *v,
                        const float2 *rope, float *k_cache, float *v_cache,
                        const DecodeShape &s, int t_count, int start,
@@ -1072,13 +1143,5 @@ void launch_attention_prefill(const float *q, const float *k_cache,
     check_launch("prefill attention");
 }
 
-void launch_silu_mul(const float *g, const float *u, _Float16 *act_hi,
-                     _Float16 *act_lo, size_t n, hipStream_t stream)
-{
-    const int blocks = int((n + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(kThreads), 0, stream,
-                       g, u, act_hi, act_lo, n);
-    check_launch("prefill silu");
-}
 
 } // namespace nut

@@ -30,6 +30,14 @@ void launch_qgemm_rows(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
                        const QMat *const *w, const uint32_t *const *stage_scales,
                        float *const *c, const int *ldc, int count, bool add,
                        hipStream_t stream);
+// act[t][n] = silu(gate[n] . x[t]) * (up[n] . x[t]) as limbs (act_hi,
+// act_lo, gate.rows values per row): both products in one launch, each
+// workgroup 64 outputs of both matrices, so neither product leaves the
+// registers.
+void launch_qgemm_swiglu(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                         const QMat &gate, const QMat &up, const uint32_t *st_gate,
+                         const uint32_t *st_up, _Float16 *act_hi, _Float16 *act_lo,
+                         hipStream_t stream);
 // RoPE of q rows and k rows at positions start + t; k and v rows into the
 // layer's cache.
 void launch_rope_store(float *q, const float *k, const float *v,
@@ -44,7 +52,5 @@ void launch_attention_prefill(const float *q, const float *k_cache,
                               const float *v_cache, _Float16 *kv_limbs, _Float16 *ctx_hi,
                               _Float16 *ctx_lo, const DecodeShape &s, int t_count,
                               hipStream_t stream);
-void launch_silu_mul(const float *g, const float *u, _Float16 *act_hi,
-                     _Float16 *act_lo, size_t n, hipStream_t stream);
 
 } // namespace nut
