@@ -212,15 +212,12 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
 {
     const nut_config &c = m.config;
     const DecodeShape &s = m.shape;
-    const size_t kvd = kv_heads_of(c) * c.head_dim;
     if (m.pf_h.get() == nullptr) {
         const size_t rows = c.max_seq;
         m.pf_h.allocate(rows * c.dim * sizeof(float));
         m.pf_x.allocate(rows * c.dim * sizeof(float));
         m.pf_act.allocate(rows * c.ffn_dim * sizeof(float));
         m.pf_q.allocate(rows * c.dim * sizeof(float));
-        m.pf_k.allocate(rows * kvd * sizeof(float));
-        m.pf_v.allocate(rows * kvd * sizeof(float));
         m.pf_ctx.allocate(rows * c.dim * sizeof(float));
         m.pf_kv.allocate(4 * prefill_kv_limb_elems(s) * sizeof(_Float16));
     }
@@ -230,7 +227,7 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
     float *h = m.pf_h.as<float>();
     _Float16 *xh = m.pf_x.as<_Float16>(), *ch = m.pf_ctx.as<_Float16>();
     _Float16 *act_h = m.pf_act.as<_Float16>();
-    float *q = m.pf_q.as<float>(), *k = m.pf_k.as<float>(), *v = m.pf_v.as<float>();
+    float *q = m.pf_q.as<float>();
     launch_embed_rows(m.embeddings.as<float>(), m.prompt.as<int>(), h, t, s.dim,
                       m.stream);
     const size_t layer_elems = kv.layer_elements();
@@ -240,16 +237,15 @@ void prefill_batch(nut_model &m, nut_kvcache &kv, size_t count)
         float *kc = kv.keys.as<float>() + l * layer_elems;
         float *vc = kv.values.as<float>() + l * layer_elems;
         const QMat *qkv_w[3] = {&w.query, &w.key, &w.value};
-        float *const qkv_c[3] = {q, k, v};
-        const int qkv_ld[3] = {s.dim, int(kvd), int(kvd)};
         const QMat *wo = &w.output, *wd = &w.down;
         launch_rmsnorm_rows(h, w.attention_norm, xh, xh + size_t(t) * s.dim, t, s.dim,
                             m.stream);
-        launch_qgemm_rows(xh, xh + size_t(t) * s.dim, t, qkv_w, ss, qkv_c, qkv_ld, 3, false,
-                          m.stream);
-        launch_rope_store(q, k, v, m.rope.as<float2>(), kc, vc, s, t, 0, m.stream);
-        launch_attention_prefill(q, kc, vc, m.pf_kv.as<_Float16>(), ch, ch + size_t(t) * s.dim,
-                                 s, t, m.stream);
+        // Q/K/V products, RoPE, the cache rows and the attention's K/V limbs
+        // in one launch
+        launch_qgemm_qkv(xh, xh + size_t(t) * s.dim, t, qkv_w, ss, q, m.rope.as<float2>(), kc,
+                         vc, m.pf_kv.as<_Float16>(), s, m.stream);
+        launch_attention_prefill(q, m.pf_kv.as<_Float16>(), ch, ch + size_t(t) * s.dim, s, t,
+                                 m.stream);
         launch_qgemm_rows(ch, ch + size_t(t) * s.dim, t, &wo, ss + 3, &h, &s.dim, 1, true,
                           m.stream);
         launch_rmsnorm_rows(h, w.ffn_norm, xh, xh + size_t(t) * s.dim, t, s.dim, m.stream);

@@ -81,7 +81,7 @@ struct nut_model {
     nut::DeviceBuffer exchange, token_error, timeline;
     nut::DeviceBuffer exchange_once; // write-once words of fused-attention launches
     // Prefill GEMM path: activations of a whole prompt, max_seq rows each.
-    nut::DeviceBuffer pf_h, pf_x, pf_q, pf_k, pf_v, pf_ctx, pf_act;
+    nut::DeviceBuffer pf_h, pf_x, pf_q, pf_ctx, pf_act;
     nut::DeviceBuffer pf_kv; // the batch's K and V as f16 limbs (prefill attention)
     nut::DeviceBuffer sample_ws; // sampling: numerators, sort buffers
     size_t timeline_entries = 0; // > 0 when the phase timeline is recorded

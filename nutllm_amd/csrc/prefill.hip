@@ -126,37 +126,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
         put(i, x[i]);
 }
 
-// RoPE on q (all heads) and k (kv heads) of token t at position start + t,
-// the rotation of the decode path (src/quant_model.cpp:26-37), then K and V
-// rows into the cache [kv_head][max_seq][head_dim] of this layer. Each
-// (even, odd) pair moves as one float2.
-__global__ __launch_bounds__(kThreads) void rope_store_kernel(
-    float *q, const float *k, const float *v, const float2 *rope, float *k_cache,
-    float *v_cache, int heads, int kv_heads, int hd, int max_seq, int start)
-{
-    const int t = blockIdx.x;
-    const int pos = start + t;
-    const int dim = heads * hd, kvd = kv_heads * hd;
-    const float2 *cs = rope + size_t(pos) * (hd / 2);
-    float2 *qr = reinterpret_cast<float2 *>(q + size_t(t) * dim);
-    for (int i = threadIdx.x; i < dim / 2; i += kThreads) {
-        const float2 f = cs[i % (hd / 2)];
-        const float2 e = qr[i];
-        qr[i] = make_float2(fmaf(e.x, f.x, -(e.y * f.y)), fmaf(e.x, f.y, e.y * f.x));
-    }
-    const float2 *kr = reinterpret_cast<const float2 *>(k + size_t(t) * kvd);
-    const float2 *vr = reinterpret_cast<const float2 *>(v + size_t(t) * kvd);
-    for (int i = threadIdx.x; i < kvd / 2; i += kThreads) {
-        const float2 f = cs[i % (hd / 2)];
-        const float2 e = kr[i];
-        const int head = (2 * i) / hd, d = (2 * i) % hd;
-        const size_t at = (size_t(head) * max_seq + pos) * hd + d;
-        *reinterpret_cast<float2 *>(k_cache + at) =
-            make_float2(fmaf(e.x, f.x, -(e.y * f.y)), fmaf(e.x, f.y, e.y * f.x));
-        *reinterpret_cast<float2 *>(v_cache + at) = vr[i];
-    }
-}
-
 // ------------------------------------- quantised GEMM on f16 MFMA --
 
 // C[t][n] (= or +=) sum_k X[t][k] W[n][k], W quantised (block 32 along k,
@@ -217,7 +186,18 @@ struct GemmSegs {
     // SwiGLU launches: w[0] gate, w[1] up; silu(gate) * up as limbs
     _Float16 *act_hi, *act_lo;
     int act_ld;
+    // Q/K/V launches (segments q, k, v): RoPE table [pos][hd / 2] (cos,
+    // sin); the layer's cache [kv_head][max_seq][hd]; the batch's K and V
+    // as f16 limbs, K [kv_head][t_pad][hd], V transposed [kv_head][hd][t_pad]
+    const float2 *rope;
+    float *k_cache, *v_cache;
+    _Float16 *k_hi, *k_lo, *vt_hi, *vt_lo;
+    int hd, max_seq, t_pad;
 };
+
+// What a GEMM launch does with its products: store, add to C (residual),
+// silu(gate) * up as limbs, or RoPE + K/V cache and limb stores.
+enum Epilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiglu = 2, kEpiQkv = 3 };
 
 // Source row of tile row r (0 .. 127) and its matrix (0 or 1): row n0 + r
 // of the segment's matrix; for a SwiGLU tile, gate and up rows alternate in
@@ -334,7 +314,7 @@ __device__ __forceinline__ half8 codes8(uint2 raw)
     return __builtin_bit_cast(half8, make_uint4(out[0], out[1], out[2], out[3]));
 }
 
-// The loader wave of qgemm_f16_kernel<QT, ADD, true>: it issues every DMA
+// The loader wave of qgemm_f16_kernel<QT, EPI, true>: it issues every DMA
 // instruction of a stage (x_hi and x_lo rows 8 i .. 8 i + 7, i < 8; the
 // weight rows, 16 (INT8) or 32 (INT4) per instruction; the scale dwords of
 // rows 64 i + lane, i < 2) into the three-slot ring, and meets the compute
@@ -418,15 +398,17 @@ __device__ __forceinline__ void qgemm_loader(const _Float16 *x_hi, const _Float1
 // 53.1 us, W2 144-147 -> 130-134 us (alternated on one box). With two
 // workgroups per CU it is slower (TinyLlama gate/up at 2,048 tokens: 256 ->
 // 292 us).
-// SWIGLU: the tile holds gate and up rows of 64 outputs (tile_row_source),
-// and the epilogue writes silu(gate) * up as limbs (act_hi, act_lo) instead
-// of the two products.
-template <int QT, bool ADD, bool LOADER, bool SWIGLU>
+// EPI (Epilogue): kEpiSwiglu tiles hold gate and up rows of 64 outputs
+// (tile_row_source) and write silu(gate) * up as limbs (act_hi, act_lo)
+// instead of the two products; kEpiQkv rotates q and k (RoPE), stores q,
+// puts k and v rows into the cache and their limbs into the attention's
+// K / V operands (zeros for the padding positions t_count .. t_pad - 1).
+template <int QT, int EPI, bool LOADER>
 __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f16_kernel(
     const _Float16 *__restrict__ x_hi, const _Float16 *__restrict__ x_lo, int t_count,
     GemmSegs segs)
 {
-    static_assert(!(ADD && SWIGLU), "one epilogue");
+    constexpr bool SWIGLU = EPI == kEpiSwiglu, ADD = EPI == kEpiAdd;
     __shared__ GemmSlot<QT> slot[kStages];
     __shared__ uint32_t junk[kWave];
     int seg = 0, tile = blockIdx.x;
@@ -684,6 +666,63 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
             }
         return;
     }
+    if constexpr (EPI == kEpiQkv) {
+        // seg 0: q, 1: k, 2: v (workgroup-uniform); a tile never straddles
+        // a head (hd is 64 or 128). RoPE as the decode step's rotation
+        // (src/quant_model.cpp:26-37) at position t: the pair (d even,
+        // d + 1) sits in lanes li, li ^ 1 of one 16-lane row.
+        const int hd = segs.hd;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + 32 * wave + 16 * j + li;
+            const int head = n / hd, d = n % hd;
+            const bool col = n < n_count;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float r[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const float val = acc[i][j][v];
+                    const float other = dpp<kDppQuadSwap1>(val, 0.0f); // lane li ^ 1
+                    const int t = t0 + 16 * i + 4 * g + v;
+                    r[v] = val;
+                    if (seg < 2) {
+                        const float2 f = segs.rope[size_t(min(t, t_count - 1)) * (hd / 2) + d / 2];
+                        r[v] = (d & 1) == 0 ? fmaf(val, f.x, -(other * f.y))
+                                            : fmaf(other, f.y, val * f.x);
+                    }
+                }
+                const int tb = t0 + 16 * i + 4 * g;
+                if (!col)
+                    continue;
+                if (seg == 0) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        if (tb + v < t_count)
+                            c[size_t(tb + v) * ldc + n] = r[v];
+                    continue;
+                }
+                float *cache = seg == 1 ? segs.k_cache : segs.v_cache;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    if (tb + v < t_count)
+                        cache[(size_t(head) * segs.max_seq + tb + v) * hd + d] = r[v];
+                    else
+                        r[v] = 0.0f; // padding positions: exact zeros
+                }
+                if (seg == 1) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        put_limbs(segs.k_hi, segs.k_lo,
+                                  (size_t(head) * segs.t_pad + tb + v) * hd + d, r[v]);
+                } else {
+                    put_limbs4(segs.vt_hi, segs.vt_lo, (size_t(head) * hd + d) * segs.t_pad + tb,
+                               make_float4(r[0], r[1], r[2], r[3]));
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -699,7 +738,7 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
             }
 }
 
-template <int QT, bool ADD, bool SWIGLU>
+template <int QT, int EPI>
 void launch_qgemm_form(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
                        const GemmSegs &segs, hipStream_t stream)
 {
@@ -709,10 +748,10 @@ void launch_qgemm_form(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
     const dim3 grid(tiles, (t_count + FM_ROWS - 1) / FM_ROWS);
     // at most one workgroup per CU (MI355X: 256 CUs): the loader-wave form
     if (size_t(grid.x) * grid.y <= 256)
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, true, SWIGLU>), grid,
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, EPI, true>), grid,
                            dim3(kThreads + kWave), 0, stream, x_hi, x_lo, t_count, segs);
     else
-        hipLaunchKernelGGL((qgemm_f16_kernel<QT, ADD, false, SWIGLU>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((qgemm_f16_kernel<QT, EPI, false>), grid, dim3(kThreads), 0,
                            stream, x_hi, x_lo, t_count, segs);
 }
 
@@ -721,9 +760,9 @@ void launch_qgemm(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
                   const GemmSegs &segs, bool add, hipStream_t stream)
 {
     if (add)
-        launch_qgemm_form<QT, true, false>(x_hi, x_lo, t_count, segs, stream);
+        launch_qgemm_form<QT, kEpiAdd>(x_hi, x_lo, t_count, segs, stream);
     else
-        launch_qgemm_form<QT, false, false>(x_hi, x_lo, t_count, segs, stream);
+        launch_qgemm_form<QT, kEpiStore>(x_hi, x_lo, t_count, segs, stream);
 }
 
 // Causal attention of a prompt batch: queries t0 .. t0 + 63 at positions
@@ -732,51 +771,6 @@ constexpr int AQ = 64, AK = 64;
 
 // Positions of the K/V limb buffers: max_seq rounded up to whole key tiles.
 int kv_limb_rows(const DecodeShape &s) { return (s.max_seq + AK - 1) / AK * AK; }
-
-// K and V of the batch's positions as f16 limbs (hi = f16(v), lo =
-// f16(v - hi)), written once per layer for the attention below: K as
-// [kv_head][pos][HD], V transposed as [kv_head][HD][pos], positions padded
-// to a multiple of 64 with zeros (a masked key then has an exact zero
-// weight times a finite value). One workgroup per (kv head, 32 positions);
-// the V tile is transposed through LDS so that reads and writes stay
-// coalesced, four values per load and per limb store.
-constexpr int kLimbTile = 32;
-
-template <int HD>
-__global__ __launch_bounds__(kThreads) void kv_limbs_kernel(
-    const float *k_cache, const float *v_cache, int max_seq, int t_count, int t_pad,
-    _Float16 *k_hi, _Float16 *k_lo, _Float16 *vt_hi, _Float16 *vt_lo)
-{
-    constexpr int P = kLimbTile, Q = HD / 4; // positions; float4s per row
-    static_assert(P * Q % kThreads == 0 && HD * (P / 4) % kThreads == 0,
-                  "whole float4s per thread");
-    static_assert(AK % P == 0, "tiles cover the padded positions");
-    __shared__ __attribute__((aligned(16))) float tile[P][HD + 4];
-    const int kvh = blockIdx.x, p0 = blockIdx.y * P;
-    const float4 *kc = reinterpret_cast<const float4 *>(k_cache + size_t(kvh) * max_seq * HD);
-    const float4 *vc = reinterpret_cast<const float4 *>(v_cache + size_t(kvh) * max_seq * HD);
-    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-    for (int u = 0; u < P * Q / kThreads; u++) {
-        const int e = threadIdx.x + kThreads * u;
-        const int p = e / Q, c = e % Q;
-        const bool in = p0 + p < t_count;
-        const size_t at = size_t(min(p0 + p, t_count - 1)) * Q + c;
-        float4 kv = kc[at], vv = vc[at];
-        if (!in)
-            kv = vv = zero;
-        put_limbs4(k_hi, k_lo, (size_t(kvh) * t_pad + p0 + p) * HD + 4 * c, kv);
-        *reinterpret_cast<float4 *>(&tile[p][4 * c]) = vv;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < HD * (P / 4) / kThreads; u++) {
-        const int e = threadIdx.x + kThreads * u;
-        const int d = e / (P / 4), p = 4 * (e % (P / 4));
-        put_limbs4(vt_hi, vt_lo, (size_t(kvh) * HD + d) * t_pad + p0 + p,
-                   make_float4(tile[p][d], tile[p + 1][d], tile[p + 2][d], tile[p + 3][d]));
-    }
-}
 
 // On v_mfma_f32_16x16x32_f16 with operands as f16 limbs: every product a b
 // is a_hi b_hi + a_hi b_lo + a_lo b_hi (three MFMAs; the dropped a_lo b_lo
@@ -1086,22 +1080,10 @@ void launch_qgemm_swiglu(const _Float16 *x_hi, const _Float16 *x_lo, int t_count
     segs.act_lo = act_lo;
     segs.act_ld = gate.rows;
     if (gate.type == 1)
-        launch_qgemm_form<1, false, true>(x_hi, x_lo, t_count, segs, stream);
+        launch_qgemm_form<1, kEpiSwiglu>(x_hi, x_lo, t_count, segs, stream);
     else
-        launch_qgemm_form<0, false, true>(x_hi, x_lo, t_count, segs, stream);
+        launch_qgemm_form<0, kEpiSwiglu>(x_hi, x_lo, t_count, segs, stream);
     check_launch("prefill gemm swiglu");
-}
-
-void launch_rope_store(float *q, const float *k, const float *v,
-                       const float2 *rope, float *k_cache, float *v_cache,
-                       const DecodeShape &s, int t_count, int start,
-                       hipStream_t stream)
-{
-    require(s.head_dim % 2 == 0, NUT_EINVAL, "prefill rope: odd head_dim");
-    hipLaunchKernelGGL(rope_store_kernel, dim3(t_count), dim3(kThreads), 0,
-                       stream, q, k, v, rope, k_cache, v_cache, s.heads,
-                       s.kv_heads, s.head_dim, s.max_seq, start);
-    check_launch("prefill rope");
 }
 
 size_t prefill_kv_limb_elems(const DecodeShape &s)
@@ -1109,39 +1091,75 @@ size_t prefill_kv_limb_elems(const DecodeShape &s)
     return size_t(s.kv_heads) * kv_limb_rows(s) * s.head_dim;
 }
 
-void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, _Float16 *kv_limbs, _Float16 *ctx_hi,
+void launch_qgemm_qkv(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                      const QMat *const *w, const uint32_t *const *stage_scales, float *q,
+                      const float2 *rope, float *k_cache, float *v_cache, _Float16 *kv_limbs,
+                      const DecodeShape &s, hipStream_t stream)
+{
+    const int kvd = s.kv_heads * s.head_dim;
+    require(s.head_dim == 64 || s.head_dim == 128, NUT_EINVAL,
+            "prefill gemm: head_dim must be 64 or 128");
+    require(w[0]->rows == s.heads * s.head_dim && w[1]->rows == kvd && w[2]->rows == kvd,
+            NUT_EINVAL, "prefill gemm: q/k/v rows do not match the shape");
+    const int t_pad = (t_count + AK - 1) / AK * AK;
+    require(t_pad <= kv_limb_rows(s) && t_count <= s.max_seq, NUT_EINVAL,
+            "prefill gemm: prompt too long");
+    GemmSegs segs{};
+    segs.count = 3;
+    for (int i = 0; i < 3; i++) {
+        require(w[i]->type == w[0]->type && w[i]->cols == w[0]->cols, NUT_EINVAL,
+                "prefill gemm: matrices differ in type or input size");
+        require(w[i]->cols % FS == 0 && stage_scales[i] != nullptr, NUT_EINVAL,
+                "prefill gemm: rows of whole 64-wide stages with stage-major scales");
+        segs.w[i] = *w[i];
+        segs.st[i] = stage_scales[i];
+        segs.tiles[i] = (w[i]->rows + FN - 1) / FN;
+    }
+    segs.c[0] = q;
+    segs.ldc[0] = s.heads * s.head_dim;
+    const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
+    segs.rope = rope;
+    segs.k_cache = k_cache;
+    segs.v_cache = v_cache;
+    segs.k_hi = kv_limbs;
+    segs.k_lo = kv_limbs + n;
+    segs.vt_hi = kv_limbs + 2 * n;
+    segs.vt_lo = kv_limbs + 3 * n;
+    segs.hd = s.head_dim;
+    segs.max_seq = s.max_seq;
+    segs.t_pad = t_pad;
+    if (w[0]->type == 1)
+        launch_qgemm_form<1, kEpiQkv>(x_hi, x_lo, t_count, segs, stream);
+    else
+        launch_qgemm_form<0, kEpiQkv>(x_hi, x_lo, t_count, segs, stream);
+    check_launch("prefill gemm qkv");
+}
+
+void launch_attention_prefill(const float *q, const _Float16 *kv_limbs, _Float16 *ctx_hi,
                               _Float16 *ctx_lo, const DecodeShape &s, int t_count,
                               hipStream_t stream)
 {
     const int t_pad = (t_count + AK - 1) / AK * AK;
     require(t_pad <= kv_limb_rows(s), NUT_EINVAL, "prefill attention: prompt too long");
     const size_t n = size_t(s.kv_heads) * t_pad * s.head_dim;
-    _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
-    const dim3 kv_grid(s.kv_heads, t_pad / kLimbTile), grid(s.heads, t_pad / AQ);
+    const _Float16 *k_hi = kv_limbs, *k_lo = k_hi + n, *vt_hi = k_lo + n, *vt_lo = vt_hi + n;
+    const dim3 grid(s.heads, t_pad / AQ);
     // head_dim 64: two query heads per workgroup when they share a KV head
     const bool pair = (s.heads / s.kv_heads) % 2 == 0;
     const dim3 pair_grid(s.heads / 2, t_pad / AQ);
-    if (s.head_dim == 128) {
-        hipLaunchKernelGGL(kv_limbs_kernel<128>, kv_grid, dim3(kThreads), 0, stream, k_cache,
-                           v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
+    if (s.head_dim == 128)
         hipLaunchKernelGGL((attention_prefill_f16<128, 1>), grid, dim3(256), 0, stream, q,
                            k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
                            s.heads, s.kv_heads, s.attn_scale);
-    } else {
-        hipLaunchKernelGGL(kv_limbs_kernel<64>, kv_grid, dim3(kThreads), 0, stream, k_cache,
-                           v_cache, s.max_seq, t_count, t_pad, k_hi, k_lo, vt_hi, vt_lo);
-        if (pair)
-            hipLaunchKernelGGL((attention_prefill_f16<64, 2>), pair_grid, dim3(512), 0, stream,
-                               q, k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
-                               s.heads, s.kv_heads, s.attn_scale);
-        else
-            hipLaunchKernelGGL((attention_prefill_f16<64, 1>), grid, dim3(256), 0, stream, q,
-                               k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
-                               s.heads, s.kv_heads, s.attn_scale);
-    }
+    else if (pair)
+        hipLaunchKernelGGL((attention_prefill_f16<64, 2>), pair_grid, dim3(512), 0, stream, q,
+                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                           s.heads, s.kv_heads, s.attn_scale);
+    else
+        hipLaunchKernelGGL((attention_prefill_f16<64, 1>), grid, dim3(256), 0, stream, q,
+                           k_hi, k_lo, vt_hi, vt_lo, ctx_hi, ctx_lo, t_count, t_pad,
+                           s.heads, s.kv_heads, s.attn_scale);
     check_launch("prefill attention");
 }
-
 
 } // namespace nut

@@ -38,18 +38,20 @@ void launch_qgemm_swiglu(const _Float16 *x_hi, const _Float16 *x_lo, int t_count
                          const QMat &gate, const QMat &up, const uint32_t *st_gate,
                          const uint32_t *st_up, _Float16 *act_hi, _Float16 *act_lo,
                          hipStream_t stream);
-// RoPE of q rows and k rows at positions start + t; k and v rows into the
-// layer's cache.
-void launch_rope_store(float *q, const float *k, const float *v,
-                       const float2 *rope, float *k_cache, float *v_cache,
-                       const DecodeShape &s, int t_count, int start,
-                       hipStream_t stream);
-// Causal attention of the t_count queries (positions 0 .. t_count - 1) over
-// cache positions 0 .. t; kv_limbs is a workspace of
-// 4 * prefill_kv_limb_elems(s) f16 (the batch's K and V as f16 limbs).
+// The batch's K and V as f16 limbs, the prefill attention's operands:
+// 4 * prefill_kv_limb_elems(s) f16 (K hi, K lo, V^T hi, V^T lo).
 size_t prefill_kv_limb_elems(const DecodeShape &s);
-void launch_attention_prefill(const float *q, const float *k_cache,
-                              const float *v_cache, _Float16 *kv_limbs, _Float16 *ctx_hi,
+// Q/K/V products of the batch (w: query, key, value) at positions 0 ..
+// t_count - 1 with RoPE applied to q and k: q rows into q ([t][heads *
+// head_dim]), k and v rows into the layer's cache, and both as limbs into
+// kv_limbs for launch_attention_prefill.
+void launch_qgemm_qkv(const _Float16 *x_hi, const _Float16 *x_lo, int t_count,
+                      const QMat *const *w, const uint32_t *const *stage_scales, float *q,
+                      const float2 *rope, float *k_cache, float *v_cache, _Float16 *kv_limbs,
+                      const DecodeShape &s, hipStream_t stream);
+// Causal attention of the t_count queries (positions 0 .. t_count - 1) over
+// positions 0 .. t, K and V from kv_limbs as launch_qgemm_qkv wrote them.
+void launch_attention_prefill(const float *q, const _Float16 *kv_limbs, _Float16 *ctx_hi,
                               _Float16 *ctx_lo, const DecodeShape &s, int t_count,
                               hipStream_t stream);
 
