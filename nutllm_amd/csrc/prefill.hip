@@ -53,6 +53,7 @@ __device__ __forceinline__ void put_limbs(_Float16 *hi, _Float16 *lo, size_t i, 
     lo[i] = (_Float16)(v - (float)a);
 }
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 
 // put_limbs of four consecutive values, i a multiple of 4: one 8-byte store
@@ -71,6 +72,19 @@ __device__ __forceinline__ void put_limbs4(_Float16 *hi, _Float16 *lo, size_t i,
     b.w = (_Float16)(v.w - (float)a.w);
     *reinterpret_cast<half4v *>(hi + i) = a;
     *reinterpret_cast<half4v *>(lo + i) = b;
+}
+
+// put_limbs of two consecutive values, i even: one 4-byte store per limb.
+__device__ __forceinline__ void put_limbs2(_Float16 *hi, _Float16 *lo, size_t i, float2 v)
+{
+    v = make_float2(settle(v.x), settle(v.y));
+    half2v a, b;
+    a.x = (_Float16)v.x;
+    a.y = (_Float16)v.y;
+    b.x = (_Float16)(v.x - (float)a.x);
+    b.y = (_Float16)(v.y - (float)a.y);
+    *reinterpret_cast<half2v *>(hi + i) = a;
+    *reinterpret_cast<half2v *>(lo + i) = b;
 }
 
 // float4s of a row each thread keeps in registers between the sum of
@@ -147,7 +161,6 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(
 constexpr int FM_ROWS = 64, FN = 128, FK = 32;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // Two quantisation codes as two f16 (exact): an offset-binary code u sits
 // in the low byte of an f16 whose high byte is 0x64, which is the value
@@ -668,56 +681,71 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
     }
     if constexpr (EPI == kEpiQkv) {
         // seg 0: q, 1: k, 2: v (workgroup-uniform); a tile never straddles
-        // a head (hd is 64 or 128). RoPE as the decode step's rotation
-        // (src/quant_model.cpp:26-37) at position t: the pair (d even,
-        // d + 1) sits in lanes li, li ^ 1 of one 16-lane row.
+        // a head (hd is 64 or 128). The pair (d even, d + 1) sits in lanes
+        // li, li ^ 1 of one 16-lane row: the even lane takes its partner's
+        // value by DPP, rotates the pair as the decode step does
+        // (src/quant_model.cpp:26-37, the host's RoPE table at position t)
+        // and stores both values.
         const int hd = segs.hd;
+        const bool even = (li & 1) == 0;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int n = n0 + 32 * wave + 16 * j + li;
             const int head = n / hd, d = n % hd;
-            const bool col = n < n_count;
+            const bool col = even && n < n_count;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float r[4];
+                float re[4], ro[4];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const float val = acc[i][j][v];
-                    const float other = dpp<kDppQuadSwap1>(val, 0.0f); // lane li ^ 1
-                    const int t = t0 + 16 * i + 4 * g + v;
-                    r[v] = val;
-                    if (seg < 2) {
-                        const float2 f = segs.rope[size_t(min(t, t_count - 1)) * (hd / 2) + d / 2];
-                        r[v] = (d & 1) == 0 ? fmaf(val, f.x, -(other * f.y))
-                                            : fmaf(other, f.y, val * f.x);
-                    }
+                    re[v] = acc[i][j][v];
+                    ro[v] = dpp<kDppQuadSwap1>(re[v], 0.0f); // lane li ^ 1
                 }
                 const int tb = t0 + 16 * i + 4 * g;
                 if (!col)
                     continue;
+                if (seg < 2) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const float2 f =
+                            segs.rope[size_t(min(tb + v, t_count - 1)) * (hd / 2) + d / 2];
+                        const float e = re[v], o = ro[v];
+                        re[v] = fmaf(e, f.x, -(o * f.y));
+                        ro[v] = fmaf(e, f.y, o * f.x);
+                    }
+                }
                 if (seg == 0) {
 #pragma unroll
                     for (int v = 0; v < 4; v++)
                         if (tb + v < t_count)
-                            c[size_t(tb + v) * ldc + n] = r[v];
+                            *reinterpret_cast<float2 *>(c + size_t(tb + v) * ldc + n) =
+                                make_float2(re[v], ro[v]);
                     continue;
                 }
                 float *cache = seg == 1 ? segs.k_cache : segs.v_cache;
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    if (tb + v < t_count)
-                        cache[(size_t(head) * segs.max_seq + tb + v) * hd + d] = r[v];
-                    else
-                        r[v] = 0.0f; // padding positions: exact zeros
+                    if (tb + v < t_count) {
+                        *reinterpret_cast<float2 *>(
+                            cache + (size_t(head) * segs.max_seq + tb + v) * hd + d) =
+                            make_float2(re[v], ro[v]);
+                    } else {
+                        re[v] = 0.0f; // padding positions: exact zeros
+                        ro[v] = 0.0f;
+                    }
                 }
                 if (seg == 1) {
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        put_limbs(segs.k_hi, segs.k_lo,
-                                  (size_t(head) * segs.t_pad + tb + v) * hd + d, r[v]);
+                        put_limbs2(segs.k_hi, segs.k_lo,
+                                   (size_t(head) * segs.t_pad + tb + v) * hd + d,
+                                   make_float2(re[v], ro[v]));
                 } else {
-                    put_limbs4(segs.vt_hi, segs.vt_lo, (size_t(head) * hd + d) * segs.t_pad + tb,
-                               make_float4(r[0], r[1], r[2], r[3]));
+                    const size_t at = (size_t(head) * hd + d) * segs.t_pad + tb;
+                    put_limbs4(segs.vt_hi, segs.vt_lo, at,
+                               make_float4(re[0], re[1], re[2], re[3]));
+                    put_limbs4(segs.vt_hi, segs.vt_lo, at + segs.t_pad,
+                               make_float4(ro[0], ro[1], ro[2], ro[3]));
                 }
             }
         }
