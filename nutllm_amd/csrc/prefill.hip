@@ -13,6 +13,8 @@
 #include "prefill.hpp"
 #include "runtime.hpp"
 
+#include <type_traits>
+
 namespace nut {
 
 namespace {
@@ -953,32 +955,44 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
                 sc[nt] = mma3(qh[kb], ql[kb], bh, bl, sc[nt]);
             }
         float corr[4];
+        // Only the diagonal tile (p0 == t0) needs the causal mask: every key
+        // of an earlier tile precedes every query of this one, so its
+        // scores and running maxima are finite (m = -inf before the first
+        // tile gives corr = 2^-inf = 0).
+        auto softmax = [&](auto masked) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            float tmax = -INFINITY;
+            for (int v = 0; v < 4; v++) {
+                float tmax = -INFINITY;
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
-                const int kpos = p0 + 16 * nt + li;
-                const float x = kpos <= qpos[v] ? sc[nt][v] * scale2 : -INFINITY;
-                sc[nt][v] = x;
-                tmax = fmaxf(tmax, x);
+                for (int nt = 0; nt < 4; nt++) {
+                    const int kpos = p0 + 16 * nt + li;
+                    const float x = !masked || kpos <= qpos[v] ? sc[nt][v] * scale2 : -INFINITY;
+                    sc[nt][v] = x;
+                    tmax = fmaxf(tmax, x);
+                }
+                tmax = row16_max(tmax);
+                const float mn = fmaxf(m[v], tmax);
+                // rows past t_count (and fully masked tiles) keep m = -inf
+                corr[v] = masked && mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[v] - mn);
+                float sum = 0.0f;
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) {
+                    const float e = masked && sc[nt][v] == -INFINITY
+                                        ? 0.0f
+                                        : __builtin_amdgcn_exp2f(sc[nt][v] - mn);
+                    const _Float16 hi = (_Float16)e;
+                    psh[wave_all][4 * lg + v][16 * nt + li] = hi;
+                    psl[wave_all][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
+                    sum += e;
+                }
+                l[v] = l[v] * corr[v] + row16_sum(sum);
+                m[v] = mn;
             }
-            tmax = row16_max(tmax);
-            const float mn = fmaxf(m[v], tmax);
-            // rows past t_count (and fully masked tiles) keep m = -inf
-            corr[v] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[v] - mn);
-            float sum = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
-                const float e = sc[nt][v] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[nt][v] - mn);
-                const _Float16 hi = (_Float16)e;
-                psh[wave_all][4 * lg + v][16 * nt + li] = hi;
-                psl[wave_all][4 * lg + v][16 * nt + li] = (_Float16)(e - (float)hi);
-                sum += e;
-            }
-            l[v] = l[v] * corr[v] + row16_sum(sum);
-            m[v] = mn;
-        }
+        };
+        if (p0 == t0) // workgroup-uniform
+            softmax(std::true_type{});
+        else
+            softmax(std::false_type{});
 #pragma unroll
         for (int dt = 0; dt < HD / 16; dt++)
 #pragma unroll
