@@ -824,8 +824,14 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     constexpr int NT = 64 * 4 * HEADS;                     // threads
     constexpr int KP = HD + 8, VP = AK + 8, PP = AK + 8; // rows padded by 16 bytes
     constexpr int KB = HD / 32;                            // 32-wide k blocks of a head
-    __shared__ __attribute__((aligned(16))) _Float16 ksh[AK][KP], ksl[AK][KP];
-    __shared__ __attribute__((aligned(16))) _Float16 vsh[HD][VP], vsl[HD][VP];
+    // K / V^T tiles: at head_dim 128 two buffers filled by DMA (tile k + 1
+    // in flight while tile k is multiplied; 161,792 bytes of LDS with P),
+    // at head_dim 64 one buffer filled from registers (below)
+    constexpr bool DMA = HD == 128;
+    constexpr int NB = DMA ? 2 : 1;
+    static_assert(!DMA || HEADS == 1, "one wave per limb array and kind");
+    __shared__ __attribute__((aligned(16))) _Float16 ksh[NB][AK][KP], ksl[NB][AK][KP];
+    __shared__ __attribute__((aligned(16))) _Float16 vsh[NB][HD][VP], vsl[NB][HD][VP];
     __shared__ __attribute__((aligned(16))) _Float16 psh[4 * HEADS][16][PP], psl[4 * HEADS][16][PP];
     const int tid = threadIdx.x, lane = tid & 63, wave_all = tid >> 6, wave = wave_all & 3;
     const int li = lane & 15, lg = lane >> 4;
@@ -880,10 +886,10 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     // pieces, PIECES per thread and array. At head_dim 64 the next tile's
     // pieces are loaded into registers while the current tile is multiplied
     // and written to LDS at the start of the next iteration (2,048 tokens:
-    // 118.7 -> 115.0 us per layer); at head_dim 128 that costs more than it
-    // hides (512 tokens: 43.1 -> 53.0 us), so the tile is copied when it is
-    // needed.
-    constexpr bool PREFETCH = HD == 64;
+    // 118.7 -> 115.0 us per layer); at head_dim 128 that cost more than it
+    // hid (512 tokens: 43.1 -> 53.0 us: 64 more VGPRs), and the tiles go
+    // by DMA into the second buffer instead.
+    constexpr bool PREFETCH = !DMA;
     constexpr int PIECES = AK * HD / 8 / NT;
     static_assert(PIECES * NT == AK * HD / 8, "whole pieces per thread");
     uint4 nkh[PIECES], nkl[PIECES], nvh[PIECES], nvl[PIECES];
@@ -901,41 +907,61 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
             nvl[r] = *reinterpret_cast<const uint4 *>(vgl + av);
         }
     };
+    // DMA of the tile at keys p0 into buffer b: wave 0 the K hi rows, 1 K
+    // lo, 2 V^T hi, 3 V^T lo. An instruction fills 1 KB of LDS, 16 bytes a
+    // lane, in the padded layout: a K row is 17 slots of 16 bytes (16 data,
+    // then the pad, which takes a copy of the row's last slot), a V^T row 9
+    // (8 data + pad); 64 x 17 and 128 x 9 slots are 17 and 18 instructions.
+    auto dma_tile = [&](int b, int p0) {
+        const int limb = wave & 1;
+        if (wave < 2) {
+            const _Float16 *src = (limb ? kgl : kgh) + size_t(p0) * HD;
+            const uint32_t base = lds_addr(limb ? &ksl[b][0][0] : &ksh[b][0][0]);
+#pragma unroll
+            for (int i = 0; i < AK * (KP / 8) / kWave; i++) {
+                const int sl = kWave * i + lane, j = sl / (KP / 8);
+                const int c = min(sl % (KP / 8), HD / 8 - 1);
+                dma16(src + j * HD + 8 * c, __builtin_amdgcn_readfirstlane(base + 1024 * i));
+            }
+        } else {
+            const _Float16 *src = (limb ? vgl : vgh) + p0;
+            const uint32_t base = lds_addr(limb ? &vsl[b][0][0] : &vsh[b][0][0]);
+#pragma unroll
+            for (int i = 0; i < HD * (VP / 8) / kWave; i++) {
+                const int sl = kWave * i + lane, d = sl / (VP / 8);
+                const int c = min(sl % (VP / 8), AK / 8 - 1);
+                dma16(src + size_t(d) * t_pad + 8 * c,
+                      __builtin_amdgcn_readfirstlane(base + 1024 * i));
+            }
+        }
+    };
+    static_assert(!DMA || (AK * (KP / 8) % kWave == 0 && HD * (VP / 8) % kWave == 0),
+                  "whole DMA instructions per array");
     if constexpr (PREFETCH)
         load_tile(0);
+    else
+        dma_tile(0, 0);
+    int b = 0; // the buffer of the current tile
     for (int p0 = 0; p0 <= last; p0 += AK) {
-        __syncthreads(); // previous tile's readers are done
-        if constexpr (PREFETCH) {
+        if constexpr (DMA) {
+            // this wave's DMA of the tile has landed, and after the barrier
+            // every wave's has and every wave is done with the other buffer
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+            if (p0 + AK <= last) // workgroup-uniform
+                dma_tile(b ^ 1, p0 + AK);
+        } else {
+            __syncthreads(); // previous tile's readers are done
 #pragma unroll
             for (int r = 0; r < PIECES; r++) {
                 const int e = tid + NT * r;
                 const int j = e / (HD / 8), c8 = e % (HD / 8);
-                *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) = nkh[r];
-                *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) = nkl[r];
+                *reinterpret_cast<uint4 *>(&ksh[0][j][8 * c8]) = nkh[r];
+                *reinterpret_cast<uint4 *>(&ksl[0][j][8 * c8]) = nkl[r];
                 const int d = e / (AK / 8), v8 = e % (AK / 8);
-                *reinterpret_cast<uint4 *>(&vsh[d][8 * v8]) = nvh[r];
-                *reinterpret_cast<uint4 *>(&vsl[d][8 * v8]) = nvl[r];
+                *reinterpret_cast<uint4 *>(&vsh[0][d][8 * v8]) = nvh[r];
+                *reinterpret_cast<uint4 *>(&vsl[0][d][8 * v8]) = nvl[r];
             }
-        } else {
-            for (int e = tid; e < AK * HD / 8; e += NT) {
-                const int j = e / (HD / 8), c8 = e % (HD / 8);
-                const size_t at = size_t(p0 + j) * HD + 8 * c8;
-                *reinterpret_cast<uint4 *>(&ksh[j][8 * c8]) =
-                    *reinterpret_cast<const uint4 *>(kgh + at);
-                *reinterpret_cast<uint4 *>(&ksl[j][8 * c8]) =
-                    *reinterpret_cast<const uint4 *>(kgl + at);
-            }
-            for (int e = tid; e < HD * AK / 8; e += NT) {
-                const int d = e / (AK / 8), c8 = e % (AK / 8);
-                const size_t at = size_t(d) * t_pad + p0 + 8 * c8;
-                *reinterpret_cast<uint4 *>(&vsh[d][8 * c8]) =
-                    *reinterpret_cast<const uint4 *>(vgh + at);
-                *reinterpret_cast<uint4 *>(&vsl[d][8 * c8]) =
-                    *reinterpret_cast<const uint4 *>(vgl + at);
-            }
-        }
-        __syncthreads();
-        if constexpr (PREFETCH) {
+            __syncthreads();
             if (p0 + AK <= last) // workgroup-uniform
                 load_tile(p0 + AK);
             // keep the loads ahead of the tile's MFMAs
@@ -950,8 +976,8 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
         for (int kb = 0; kb < KB; kb++)
 #pragma unroll
             for (int nt = 0; nt < 4; nt++) {
-                const half8 bh = *reinterpret_cast<const half8 *>(&ksh[16 * nt + li][32 * kb + 8 * lg]);
-                const half8 bl = *reinterpret_cast<const half8 *>(&ksl[16 * nt + li][32 * kb + 8 * lg]);
+                const half8 bh = *reinterpret_cast<const half8 *>(&ksh[b][16 * nt + li][32 * kb + 8 * lg]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&ksl[b][16 * nt + li][32 * kb + 8 * lg]);
                 sc[nt] = mma3(qh[kb], ql[kb], bh, bl, sc[nt]);
             }
         float corr[4];
@@ -1009,11 +1035,13 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
             const half8 al = *reinterpret_cast<const half8 *>(&psl[wave_all][li][32 * kb + 8 * lg]);
 #pragma unroll
             for (int dt = 0; dt < HD / 16; dt++) {
-                const half8 bh = *reinterpret_cast<const half8 *>(&vsh[16 * dt + li][32 * kb + 8 * lg]);
-                const half8 bl = *reinterpret_cast<const half8 *>(&vsl[16 * dt + li][32 * kb + 8 * lg]);
+                const half8 bh = *reinterpret_cast<const half8 *>(&vsh[b][16 * dt + li][32 * kb + 8 * lg]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&vsl[b][16 * dt + li][32 * kb + 8 * lg]);
                 o[dt] = mma3(ah, al, bh, bl, o[dt]);
             }
         }
+        if constexpr (DMA)
+            b ^= 1;
     }
 #pragma unroll
     for (int v = 0; v < 4; v++) {
