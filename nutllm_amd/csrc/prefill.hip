@@ -827,9 +827,8 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     // K / V^T tiles: at head_dim 128 two buffers filled by DMA (tile k + 1
     // in flight while tile k is multiplied; 161,792 bytes of LDS with P),
     // at head_dim 64 one buffer filled from registers (below)
-    constexpr bool DMA = HD == 128;
+    constexpr bool DMA = HD == 128 || HEADS == 2;
     constexpr int NB = DMA ? 2 : 1;
-    static_assert(!DMA || HEADS == 1, "one wave per limb array and kind");
     __shared__ __attribute__((aligned(16))) _Float16 ksh[NB][AK][KP], ksl[NB][AK][KP];
     __shared__ __attribute__((aligned(16))) _Float16 vsh[NB][HD][VP], vsl[NB][HD][VP];
     __shared__ __attribute__((aligned(16))) _Float16 psh[4 * HEADS][16][PP], psl[4 * HEADS][16][PP];
@@ -913,6 +912,8 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     // then the pad, which takes a copy of the row's last slot), a V^T row 9
     // (8 data + pad); 64 x 17 and 128 x 9 slots are 17 and 18 instructions.
     auto dma_tile = [&](int b, int p0) {
+        if (wave_all >= 4) // the second head's waves issue none
+            return;
         const int limb = wave & 1;
         if (wave < 2) {
             const _Float16 *src = (limb ? kgl : kgh) + size_t(p0) * HD;
