@@ -824,9 +824,13 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
     constexpr int NT = 64 * 4 * HEADS;                     // threads
     constexpr int KP = HD + 8, VP = AK + 8, PP = AK + 8; // rows padded by 16 bytes
     constexpr int KB = HD / 32;                            // 32-wide k blocks of a head
-    // K / V^T tiles: at head_dim 128 two buffers filled by DMA (tile k + 1
-    // in flight while tile k is multiplied; 161,792 bytes of LDS with P),
-    // at head_dim 64 one buffer filled from registers (below)
+    // K / V^T tiles: at head_dim 128, and for two heads per workgroup, two
+    // buffers filled by DMA (tile k + 1 in flight while tile k is
+    // multiplied; 161,792 and 110,592 bytes of LDS with P); the one-head
+    // head_dim-64 form keeps one buffer filled from registers (below).
+    // Measured against the register forms: 512 tokens at head_dim 128
+    // 43.8 -> 31.0 us per layer, 2,048 tokens with head pairs 111.5 ->
+    // 105.1 us (one workgroup per CU instead of two).
     constexpr bool DMA = HD == 128 || HEADS == 2;
     constexpr int NB = DMA ? 2 : 1;
     __shared__ __attribute__((aligned(16))) _Float16 ksh[NB][AK][KP], ksl[NB][AK][KP];
@@ -882,12 +886,11 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
     };
     // The K tile rows p0 .. p0 + 63 and the V^T tile [d][p0 ..] in 16-byte
-    // pieces, PIECES per thread and array. At head_dim 64 the next tile's
+    // pieces, PIECES per thread and array. Without DMA the next tile's
     // pieces are loaded into registers while the current tile is multiplied
-    // and written to LDS at the start of the next iteration (2,048 tokens:
-    // 118.7 -> 115.0 us per layer); at head_dim 128 that cost more than it
-    // hid (512 tokens: 43.1 -> 53.0 us: 64 more VGPRs), and the tiles go
-    // by DMA into the second buffer instead.
+    // and written to LDS at the start of the next iteration (2,048 tokens
+    // with head pairs: 118.7 -> 115.0 us per layer; at head_dim 128 it cost
+    // more than it hid, 43.1 -> 53.0 us, for 64 more VGPRs).
     constexpr bool PREFETCH = !DMA;
     constexpr int PIECES = AK * HD / 8 / NT;
     static_assert(PIECES * NT == AK * HD / 8, "whole pieces per thread");
@@ -907,10 +910,12 @@ __global__ __launch_bounds__(64 * 4 * HEADS) void attention_prefill_f16(
         }
     };
     // DMA of the tile at keys p0 into buffer b: wave 0 the K hi rows, 1 K
-    // lo, 2 V^T hi, 3 V^T lo. An instruction fills 1 KB of LDS, 16 bytes a
-    // lane, in the padded layout: a K row is 17 slots of 16 bytes (16 data,
-    // then the pad, which takes a copy of the row's last slot), a V^T row 9
-    // (8 data + pad); 64 x 17 and 128 x 9 slots are 17 and 18 instructions.
+    // lo, 2 V^T hi, 3 V^T lo (the first head's waves). An instruction fills
+    // 1 KB of LDS, 16 bytes a lane, in the padded layout: a K row is HD / 8
+    // + 1 slots of 16 bytes (the data, then the pad, which takes a copy of
+    // the row's last slot), a V^T row 9 (8 data + pad); at head_dim 128,
+    // 64 x 17 and 128 x 9 slots are 17 and 18 instructions, at head_dim 64
+    // nine each.
     auto dma_tile = [&](int b, int p0) {
         if (wave_all >= 4) // the second head's waves issue none
             return;
