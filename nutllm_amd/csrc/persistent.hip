@@ -312,6 +312,8 @@ template <class G> struct Lds {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
     static_assert(kWaves * G::HPW * G::NP >= kScreenRowsMax,
                   "the screened classifier's upper bounds fit the scores region");
+    static_assert(kWaves * G::HPW * G::NP >= G::ROWS_GU,
+                  "phase C's gate and up results fit the scores region");
     static_assert(G::R1 >= 4 * G::DIM && G::DIM + 2 * G::KVD >= G::DIM / 32,
                   "the classifier's x in region 1, its block sums of |x| over q/k/v");
 };
@@ -765,22 +767,32 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 11 + 13 * l);
             {
+                // the workgroup's gate rows, then its up rows, one at a time
+                // over the waves: 2 np rows spread evenly over the CU's four
+                // SIMDs (whole pairs were not: 6, 6, 5, 5 of 22), each result
+                // into the scores region (free until the next attention);
+                // silu(gate) * up after the barrier
                 XDigits<G::CPL_DIM> x;
                 load_x(x, xl, xsc, G::BLK_DIM);
-                for (int pair = wave; pair < gu_e - gu_b; pair += kWaves) {
-                    const uint8_t *dg, *du;
-                    const uint16_t *sg, *su;
-                    slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, pair, dg, sg, r1);
-                    slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, G::ROWS_GU / 2 + pair, du, su, r1);
-                    const float g = row_dot<G::QT>(dg, sg, x, G::BLK_DIM);
-                    const float u = row_dot<G::QT>(du, su, x, G::BLK_DIM);
-                    if (lane == 0) {
-                        put_once(xo + ON_GU + gu_b + pair, g / (1.0f + expf(-g)) * u);
-                    }
+                const int np = gu_e - gu_b;
+                for (int r = wave; r < 2 * np; r += kWaves) {
+                    const uint8_t *d;
+                    const uint16_t *sc;
+                    slot(G::ROWS_GU, G::RB_DIM, G::SB_DIM, r < np ? r : G::ROWS_GU / 2 + r - np,
+                         d, sc, r1);
+                    const float y = row_dot<G::QT>(d, sc, x, G::BLK_DIM);
+                    if (lane == 0)
+                        scores[r] = y;
                 }
             }
-            tag++;
+            // every wave is past its reads of region 1 (the down rows go
+            // there next) and its gate / up results are in LDS
             __syncthreads();
+            if (threadIdx.x < gu_e - gu_b) {
+                const float g = scores[threadIdx.x], u = scores[gu_e - gu_b + threadIdx.x];
+                put_once(xo + ON_GU + gu_b + threadIdx.x, g / (1.0f + expf(-g)) * u);
+            }
+            tag++;
             mark(it, 12 + 13 * l);
             stage_down(l);
             mark(it, 13 + 13 * l);
