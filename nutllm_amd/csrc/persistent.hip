@@ -312,8 +312,9 @@ template <class G> struct Lds {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
     static_assert(kWaves * G::HPW * G::NP >= kScreenRowsMax,
                   "the screened classifier's upper bounds fit the scores region");
-    static_assert(kWaves * G::HPW * G::NP >= G::ROWS_GU,
-                  "phase C's gate and up results fit the scores region");
+    static_assert(kWaves * G::HPW * G::NP >= G::ROWS_GU &&
+                      kWaves * G::HPW * G::NP >= G::GR_WG,
+                  "phase A's q/k/v and phase C's gate and up results fit the scores region");
     static_assert(G::R1 >= 4 * G::DIM && G::DIM + 2 * G::KVD >= G::DIM / 32,
                   "the classifier's x in region 1, its block sums of |x| over q/k/v");
 };
@@ -541,10 +542,11 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
                 kvh = grp;
                 xrow = grp * G::GR + lr;
             };
+            // (thread p < npairs publishes pair p)
             float2 rope_cs = make_float2(1.0f, 0.0f);
-            if (wave < npairs) {
+            if (threadIdx.x < npairs) {
                 int xrow, which, d, kvh;
-                qkv_row(wave, xrow, which, d, kvh);
+                qkv_row(threadIdx.x, xrow, which, d, kvh);
                 if (which < 2)
                     rope_cs = a.rope[size_t(pos) * (G::HD / 2) + d / 2];
             }
@@ -563,39 +565,45 @@ __global__ __launch_bounds__(kThreads, 1) void token_kernel(TokenArgs a)
             stage_x<G::QT, G::DIM>(h_raw, nw4, rms_scale(wg_sum(sq, red), G::DIM), xl, xsc);
             mark(it, 4 + 13 * l);
             {
+                // the workgroup's rows one at a time over the waves (10 rows:
+                // at most three on a SIMD, where whole pairs put four on one),
+                // each result into the scores region (free until attention)
                 XDigits<G::CPL_DIM> x;
                 load_x(x, xl, xsc, G::BLK_DIM);
-                for (int pair = wave; pair < npairs; pair += kWaves) {
-                    const uint8_t *d0, *d1;
-                    const uint16_t *s0, *s1;
-                    slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, 2 * pair, d0, s0, r1);
-                    slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, 2 * pair + 1, d1, s1, r1);
-                    float e0 = row_dot<G::QT>(d0, s0, x, G::BLK_DIM);
-                    float e1 = row_dot<G::QT>(d1, s1, x, G::BLK_DIM);
-                    if (lane == 0) {
-                        int row, which, d, head;
-                        qkv_row(pair, row, which, d, head);
-                        if (which < 2) {
-                            const float2 cs = pair == wave ? rope_cs
-                                : a.rope[size_t(pos) * (G::HD / 2) + d / 2];
-                            const float even = e0, odd = e1;
-                            e0 = fmaf(even, cs.x, -(odd * cs.y));
-                            e1 = fmaf(even, cs.y, odd * cs.x);
-                        }
-                        put_once(xo + row, e0);
-                        put_once(xo + row + 1, e1);
-                        if (which > 0) {
-                            float *cache = (which == 1 ? kc : vc) +
-                                           (size_t(head) * a.max_seq + pos) * G::HD + d;
-                            store_coherent(cache, e0);
-                            store_coherent(cache + 1, e1);
-                        }
-                    }
+                for (int r = wave; r < 2 * npairs; r += kWaves) {
+                    const uint8_t *d;
+                    const uint16_t *sc;
+                    slot(G::ROWS_QKV, G::RB_DIM, G::SB_DIM, r, d, sc, r1);
+                    const float y = row_dot<G::QT>(d, sc, x, G::BLK_DIM);
+                    if (lane == 0)
+                        scores[r] = y;
+                }
+            }
+            __syncthreads();
+            // pair p: RoPE (q and k rows), the exchange words, the cache row
+            if (threadIdx.x < npairs) {
+                const int pair = threadIdx.x;
+                int row, which, d, head;
+                qkv_row(pair, row, which, d, head);
+                float e0 = scores[2 * pair], e1 = scores[2 * pair + 1];
+                if (which < 2) {
+                    const float even = e0, odd = e1;
+                    e0 = fmaf(even, rope_cs.x, -(odd * rope_cs.y));
+                    e1 = fmaf(even, rope_cs.y, odd * rope_cs.x);
+                }
+                put_once(xo + row, e0);
+                put_once(xo + row + 1, e1);
+                if (which > 0) {
+                    float *cache = (which == 1 ? kc : vc) +
+                                   (size_t(head) * a.max_seq + pos) * G::HD + d;
+                    store_coherent(cache, e0);
+                    store_coherent(cache + 1, e1);
                 }
             }
             tag++;
             // K/V rows of earlier positions stream into LDS while the q/k/v
-            // exchange completes.
+            // exchange completes (every wave is past its reads of region 1
+            // and of the scores region's row results).
             __syncthreads();
             mark(it, 5 + 13 * l);
             const int n = pos + 1;
