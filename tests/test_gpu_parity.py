@@ -505,6 +505,39 @@ def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
         assert ids == ref_ids
 
 
+@pytest.mark.parametrize("qtype", [0, 1], ids=["int8", "int4"])
+def test_prefill_gemm_fills_the_cache(gpu, qtype):
+    """A batched prefill of exactly max_seq tokens (max_seq 192: three full
+    64-query attention tiles, the attention's K/V limb rows used to the
+    last): hidden state and the first and last positions' K/V rows within
+    rel-L2 2e-3 of the step kernels, and the next decode step then fails
+    with the reference's full-cache error."""
+    model = W.build("tinyllama", qtype, 5, 192)
+    c = model.config
+    prompt = gpu.synth_tokens(29, c.vocab_size, c.max_seq)
+    dev = model.to_device()
+    try:
+        cache = gpu.KVCache(c)
+        h = dev.prefill(cache, prompt)
+        dev.set_path(1)
+        ref_cache = gpu.KVCache(c)
+        ref = dev.prefill(ref_cache, prompt)
+        dev.set_path(0)
+        err = rel_l2(h, ref)
+        print(f"prefill of max_seq tokens: hidden rel-L2 {err:.2e}", flush=True)
+        assert err <= PREFILL_TOL
+        for layer in (0, c.layers - 1):
+            for kvh in range(c.kv_heads):
+                for p in (0, c.max_seq - 1):
+                    k, v = cache.key_value(layer, kvh, p)
+                    rk, rv = ref_cache.key_value(layer, kvh, p)
+                    assert rel_l2(k, rk) <= PREFILL_TOL and rel_l2(v, rv) <= PREFILL_TOL
+        with pytest.raises(gpu.LengthError, match="context is full"):
+            dev.decode(cache, 0)
+    finally:
+        dev.close()
+
+
 @pytest.mark.parametrize("shape,qtype", [("step_mha128", 1), ("step_gqa4", 0)],
                          ids=["mha128-int4", "gqa4-int8"])
 def test_prefill_gemm_other_heads(gpu, shape, qtype):
