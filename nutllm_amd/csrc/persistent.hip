@@ -57,9 +57,12 @@ namespace {
 // 484.7. The classifier's input (the last layer's h after W2), swept on
 // TinyLlama INT4 once the generate loop no longer read the error flag in
 // a round trip of its own before it (three runs each): none 345.6 us per
-// token, 300 ns 344.0, 600 ns 344.0.
+// token, 300 ns 344.0, 600 ns 344.0. Once phases A and C published after
+// a barrier (two runs each, one box): B 0, 50, 150 ns 340.3-340.8,
+// 340.2-340.2, 339.4-339.7 us per token (150 ns kept); A 150, 300,
+// 450 ns 339.6-340.5, 340.2, 343.9-344.2.
 template <bool LONG> struct PollDelay {
-    static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 5;
+    static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 15;
     static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 60;
     static constexpr int PARTIALS = 90, CONTEXT = 90;
     static constexpr int CLASSIFIER = 60;
