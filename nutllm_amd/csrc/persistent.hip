@@ -60,10 +60,13 @@ namespace {
 // token, 300 ns 344.0, 600 ns 344.0. Once phases A and C published after
 // a barrier (two runs each, one box): B 0, 50, 150 ns 340.3-340.8,
 // 340.2-340.2, 339.4-339.7 us per token (150 ns kept); A 150, 300,
-// 450 ns 339.6-340.5, 340.2, 343.9-344.2.
+// 450 ns 339.6-340.5, 340.2, 343.9-344.2; then D (three runs each) 600,
+// 750, 900, 1,050 ns 338.4-339.4, 336.1-336.8, 338.6-340.4, 345.9-348.2
+// (750 ns kept; the act exchange 1.62 -> 1.49 us), C 50, 300 ns no
+// better than 150; with split attention D 450, 900 ns no better than 600.
 template <bool LONG> struct PollDelay {
     static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 15;
-    static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 60;
+    static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 75;
     static constexpr int PARTIALS = 90, CONTEXT = 90;
     static constexpr int CLASSIFIER = 60;
 };
