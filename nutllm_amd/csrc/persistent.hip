@@ -63,7 +63,9 @@ namespace {
 // 450 ns 339.6-340.5, 340.2, 343.9-344.2; then D (three runs each) 600,
 // 750, 900, 1,050 ns 338.4-339.4, 336.1-336.8, 338.6-340.4, 345.9-348.2
 // (750 ns kept; the act exchange 1.62 -> 1.49 us), C 50, 300 ns no
-// better than 150; with split attention D 450, 900 ns no better than 600.
+// better than 150; with split attention D 450, 900 ns no better than 600,
+// and A 450 / 750, B 150 / 450, C 150 / 450 ns all within 0.5 us of
+// 469.5-469.8 us per token (INT8 at KV 2048-2175).
 template <bool LONG> struct PollDelay {
     static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 15;
     static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 75;
