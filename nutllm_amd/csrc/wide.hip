@@ -119,10 +119,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // written yet. Measured on the Llama-2-7B shape (128 tokens at KV 512-639):
 // none 1,639 us per token; scores 300 ns + context 600 ns 1,627; 1.2 +
 // 2.4 us 1,596-1,597; 1.8 + 2.4 us 1,605; 2.4 + 2.4 us 1,623; 1.2 + 3.6 us
-// 1,631. The other three exchanges (h into A, h after Wo, act) wait behind
-// their phase's weight DMA already; 600 ns more on them cost 9 us.
+// 1,631. Re-swept with write-once words and the ring (two runs each, one
+// box): scores 0.9 / 1.2 / 1.5 us 1,555.3-1,556.0 / 1,548.7-1,549.3 /
+// 1,551.7-1,553.5; context 0.8 / 1.2 / 1.6 / 2.0 / 2.4 / 2.8 us
+// 1,552.8-1,553.4 / 1,551.3-1,552.4 / 1,548.9-1,549.8 / 1,545.9-1,547.6 /
+// 1,547.8-1,549.3 / 1,559.3-1,559.4 (2.0 kept). The other three exchanges
+// (h into A, h after Wo, act) wait behind their phase's weight DMA
+// already; 600 ns more on them cost 9 us.
 constexpr int kWidePollDelayScores = 120;
-constexpr int kWidePollDelayContext = 240;
+constexpr int kWidePollDelayContext = 200;
 // The classifier's input (the last layer's h after W2): 600 ns as in the
 // TinyLlama-shape kernel (1,548.8 against 1,549.7 us per token with none).
 constexpr int kWidePollDelayClassifier = 60;
