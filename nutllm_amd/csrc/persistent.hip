@@ -65,12 +65,14 @@ namespace {
 // (750 ns kept; the act exchange 1.62 -> 1.49 us), C 50, 300 ns no
 // better than 150; with split attention D 450, 900 ns no better than 600,
 // and A 450 / 750, B 150 / 450, C 150 / 450 ns all within 0.5 us of
-// 469.5-469.8 us per token (INT8 at KV 2048-2175).
+// 469.5-469.8 us per token (INT8 at KV 2048-2175). The classifier's input
+// then (three runs each): 300, 600, 900 ns 335.8-336.5, 337.1-338.1,
+// 336.1-337.1 us per token (300 ns kept).
 template <bool LONG> struct PollDelay {
     static constexpr int A = LONG ? 60 : 30, B = LONG ? 30 : 15;
     static constexpr int C = LONG ? 30 : 15, D = LONG ? 60 : 75;
     static constexpr int PARTIALS = 90, CONTEXT = 90;
-    static constexpr int CLASSIFIER = 60;
+    static constexpr int CLASSIFIER = 30;
 };
 
 template <int QT_, int DIM_, int FFN_, int HEADS_, int KVH_, int HD_, int NP_>
