@@ -1,9 +1,10 @@
 // prefill.hip — the prompt as a batch: prefill_quantized
 // (src/quant_model.cpp:208-220) computes, token after token, the decode
 // step of src/quant_model.cpp:158-206; this file computes the same function
-// for all T prompt tokens at once, layer by layer:
-//   rmsnorm rows -> Q/K/V GEMMs -> RoPE + KV-cache store -> causal attention
-//   -> Wo GEMM (+ residual) -> rmsnorm rows -> gate/up GEMMs -> silu * up
+// for all T prompt tokens at once, layer by layer, in six launches:
+//   rmsnorm rows -> Q/K/V GEMM (epilogue: RoPE, q, the KV-cache rows and
+//   the attention's K/V limbs) -> causal attention -> Wo GEMM (+ residual)
+//   -> rmsnorm rows -> gate/up GEMM (epilogue: silu(gate) * up as limbs)
 //   -> W2 GEMM (+ residual)
 // The quantised GEMMs run on f16 MFMA with the weight codes exact in f16,
 // the activations split into two f16 limbs and the block scales applied
@@ -666,7 +667,7 @@ __global__ __launch_bounds__(LOADER ? kThreads + kWave : kThreads) void qgemm_f1
     add_pending();
     if constexpr (SWIGLU) {
         // acc[i][0]: gate, acc[i][1]: up of output n0 + 16 wave + li
-        // (silu as silu_mul_kernel: src/quant_model.cpp:197-200)
+        // (silu as the decode step: src/quant_model.cpp:197-200)
         const int n = n0 + 16 * wave + li;
 #pragma unroll
         for (int i = 0; i < 4; i++)
