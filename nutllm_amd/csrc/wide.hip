@@ -125,7 +125,10 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // 1,552.8-1,553.4 / 1,551.3-1,552.4 / 1,548.9-1,549.8 / 1,545.9-1,547.6 /
 // 1,547.8-1,549.3 / 1,559.3-1,559.4 (2.0 kept). The other three exchanges
 // (h into A, h after Wo, act) wait behind their phase's weight DMA
-// already; 600 ns more on them cost 9 us.
+// already; 600 ns more on all three cost 9 us. Alone, two runs each: act
+// none / 300 / 600 / 900 ns 1,549.8-1,550.9 / 1,553.3-1,554.3 /
+// 1,559.5-1,560.8 / 1,562.3-1,563.0; h after Wo 300 / 600 ns
+// 1,549.8-1,552.6 / 1,558.3-1,558.5 (none kept on both).
 constexpr int kWidePollDelayScores = 120;
 constexpr int kWidePollDelayContext = 200;
 // The classifier's input (the last layer's h after W2): 600 ns as in the
