@@ -64,7 +64,7 @@ PUBLISHED_DECODE_TOK_S = 17.089  # reference, TinyLlama INT4, 4 threads
 CPU_SAMPLE_SECONDS = 8.0
 TRAFFIC_PASS_TIMEOUT = 180  # seconds per rocprofv3 counter pass
 CALIBRATE_MIB = 1024
-MAX_THREADS = 16  # the GPU box's CPU share
+MAX_THREADS = 16  # host threads for the CPU baseline (the CPU share of one GPU's host)
 
 
 def log(*a):
