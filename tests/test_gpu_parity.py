@@ -469,13 +469,15 @@ def test_tinyllama_int4_prefill_step_chunk(gpu, tinyllama_int4, prompt_len):
 PREFILL_TOL = 2e-3  # rel-L2, batched (GEMM) prefill
 
 
-@pytest.mark.parametrize("prompt_len", [40, 130, 300])
+@pytest.mark.parametrize("prompt_len", [16, 40, 64, 130, 300])
 def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
     """Prompts of 16+ tokens run as a batch (MFMA GEMMs, causal attention).
     Hidden state and K/V rows within rel-L2 2e-3 of the fp32 step arithmetic
-    (oracle for 40 tokens, the device step kernels for 130 and 300: one,
-    three and five 64-query attention tiles), and the greedy ids that follow
-    the prefill identical to the oracle's."""
+    (oracle for 16 and 40 tokens, the device step kernels for 64, 130 and
+    300: one whole 64-query attention tile with no padding, then three and
+    five tiles), and the greedy ids that follow the prefill identical to the
+    oracle's. 16 tokens is the shortest batched prompt (48 padding rows in
+    its tile)."""
     model, _, _, dev = tinyllama_int4
     prompt = gpu.synth_tokens(11, model.config.vocab_size, prompt_len)
     cache = gpu.KVCache(model.config)
