@@ -604,8 +604,10 @@ void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
     // Four rows per wave where that still gives every CU a workgroup, and
     // for prompt chunks of 8+ tokens, whose workgroups would otherwise take
     // several rounds of the chip's wave slots (TinyLlama INT4, Q/K/V and
-    // gate/up both at four: 8 tokens 1.296 -> 1.255 ms, 15 tokens 1.987 ->
-    // 1.91 ms per prompt; 5 tokens unchanged, 2 tokens 0.740 -> 0.753 ms).
+    // gate/up at four: 8 tokens 1.296 -> 1.255 ms, 15 tokens 1.987 -> 1.91
+    // ms per prompt; 5 tokens unchanged, 2 tokens 0.740 -> 0.753 ms; Wo
+    // and W2 at four too: 8 tokens 1.259 -> 1.226 ms, 15 tokens 1.915 ->
+    // 1.854 ms).
     const bool wide_chunk = CHUNK && tokens >= 8;
     if ((qkv_rows >= 8192 || wide_chunk) && s.dim % 4 == 0 && kvd % 4 == 0) {
         const int blocks = blocks_for_rows(qkv_rows, 4);
@@ -621,10 +623,19 @@ void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
                            b.query, blocks, tokens, state);
     }
     launch_attention_g<HD>(s, k_layer, v_layer, length, b, tokens, state, stream);
-    const int dim_blocks = blocks_for_rows(s.dim, 2);
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2, CHUNK>), row_grid(dim_blocks, tokens, CHUNK),
-                       dim3(kThreads), x_dim, stream, w.output, b.context, b.hidden, dim_blocks,
-                       tokens, state);
+    // Wo and W2 + residual: four rows per wave for chunks of 8+ tokens
+    const int dim_blocks = blocks_for_rows(s.dim, wide_chunk ? 4 : 2);
+    auto residual = [&](const QMat &m, const float *x, size_t x_bytes) {
+        if (wide_chunk)
+            hipLaunchKernelGGL((residual_fast_kernel<QT, 4, CHUNK>),
+                               row_grid(dim_blocks, tokens, CHUNK), dim3(kThreads), x_bytes,
+                               stream, m, x, b.hidden, dim_blocks, tokens, state);
+        else
+            hipLaunchKernelGGL((residual_fast_kernel<QT, 2, CHUNK>),
+                               row_grid(dim_blocks, tokens, CHUNK), dim3(kThreads), x_bytes,
+                               stream, m, x, b.hidden, dim_blocks, tokens, state);
+    };
+    residual(w.output, b.context, x_dim);
     if (s.ffn_dim >= 8192 || wide_chunk) {
         const int blocks = blocks_for_rows(s.ffn_dim, 4);
         hipLaunchKernelGGL((gate_up_fast_kernel<QT, 4, CHUNK>), row_grid(blocks, tokens, CHUNK),
@@ -636,9 +647,7 @@ void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
                            dim3(kThreads), x_dim, stream, b.hidden, w.ffn_norm, w.gate, w.up,
                            b.act, blocks, tokens, state);
     }
-    hipLaunchKernelGGL((residual_fast_kernel<QT, 2, CHUNK>), row_grid(dim_blocks, tokens, CHUNK),
-                       dim3(kThreads), x_ffn, stream, w.down, b.act, b.hidden, dim_blocks,
-                       tokens, state);
+    residual(w.down, b.act, x_ffn);
     check_launch("decode step");
 }
 
