@@ -602,13 +602,13 @@ void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
     const size_t x_dim = staged_x_bytes<QT>(s.dim), x_ffn = staged_x_bytes<QT>(s.ffn_dim);
     const int qkv_rows = s.dim + 2 * kvd;
     // Four rows per wave where that still gives every CU a workgroup, and
-    // for prompt chunks of 8+ tokens, whose workgroups would otherwise take
-    // several rounds of the chip's wave slots (TinyLlama INT4, Q/K/V and
-    // gate/up at four: 8 tokens 1.296 -> 1.255 ms, 15 tokens 1.987 -> 1.91
-    // ms per prompt; 5 tokens unchanged, 2 tokens 0.740 -> 0.753 ms; Wo
-    // and W2 at four too: 8 tokens 1.259 -> 1.226 ms, 15 tokens 1.915 ->
-    // 1.854 ms).
-    const bool wide_chunk = CHUNK && tokens >= 8;
+    // for prompt chunks of 6+ tokens, whose workgroups would otherwise take
+    // several rounds of the chip's wave slots. TinyLlama INT4 prompts, every
+    // row launch at four rows per wave against two: 15 tokens 1.987 ->
+    // 1.854 ms, 8 tokens 1.296 -> 1.226, 7 tokens 1.216 -> 1.165, 6 tokens
+    // 1.090 -> 1.070; but 5 tokens 0.998 -> 1.013, 4 tokens 0.893 -> 0.917,
+    // 3 tokens 0.818 -> 0.850.
+    const bool wide_chunk = CHUNK && tokens >= 6;
     if ((qkv_rows >= 8192 || wide_chunk) && s.dim % 4 == 0 && kvd % 4 == 0) {
         const int blocks = blocks_for_rows(qkv_rows, 4);
         hipLaunchKernelGGL((qkv_fast_kernel<QT, 4, CHUNK>), row_grid(blocks, tokens, CHUNK),
@@ -623,7 +623,7 @@ void launch_layer_fast_c(const DecodeShape &s, const LayerView &w,
                            b.query, blocks, tokens, state);
     }
     launch_attention_g<HD>(s, k_layer, v_layer, length, b, tokens, state, stream);
-    // Wo and W2 + residual: four rows per wave for chunks of 8+ tokens
+    // Wo and W2 + residual: four rows per wave for chunks of 6+ tokens
     const int dim_blocks = blocks_for_rows(s.dim, wide_chunk ? 4 : 2);
     auto residual = [&](const QMat &m, const float *x, size_t x_bytes) {
         if (wide_chunk)

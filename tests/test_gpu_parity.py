@@ -443,12 +443,13 @@ def test_tiny_matches_reference_golden(gpu, qtype, tag, norms):
     dev.close()
 
 
-@pytest.mark.parametrize("prompt_len", [2, 5, 15])
+@pytest.mark.parametrize("prompt_len", [2, 5, 6, 15])
 def test_tinyllama_int4_prefill_step_chunk(gpu, tinyllama_int4, prompt_len):
     """Prompts below the GEMM threshold run as one chunk of consecutive
     tokens through the step kernels (each launch covers every token; the
-    arithmetic per token is the decode step's). Hidden state and K/V rows
-    within rel-L2 1e-5 of the oracle's per-token prefill."""
+    arithmetic per token is the decode step's; from 6 tokens the row
+    launches take four rows per wave). Hidden state and K/V rows within
+    rel-L2 1e-5 of the oracle's per-token prefill."""
     model, _, _, dev = tinyllama_int4
     prompt = gpu.synth_tokens(17, model.config.vocab_size, prompt_len)
     cache = gpu.KVCache(model.config)
