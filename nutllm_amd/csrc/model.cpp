@@ -190,10 +190,11 @@ void prefill_steps(nut_model &m, nut_kvcache &kv, size_t count)
 }
 
 // Prompts of at least this many tokens run as a batch (GEMM prefill);
-// shorter ones run as step-kernel chunks of up to 15 tokens. TinyLlama INT4,
-// batch against chunks: 16 tokens 3.02 against 2.46 ms, 22 tokens 3.10
-// against 2.98, 24 tokens 3.10 against 3.17, 32 tokens 3.11 against 4.39.
-constexpr size_t kPrefillGemmMin = 24;
+// shorter ones run as one step-kernel chunk (kStepTokensMax = 31).
+// TinyLlama INT4, batch against one chunk: 16 tokens 1.95 against 1.94 ms,
+// 24 tokens 3.11 against 2.64, 28 tokens 3.12 against 2.94, 31 tokens 3.12
+// against 3.16.
+constexpr size_t kPrefillGemmMin = 30;
 
 // The batched prefill applies when every layer uses 32-wide blocks, the
 // head size matches its attention tiles, and per-token steps are not

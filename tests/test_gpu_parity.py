@@ -443,14 +443,13 @@ def test_tiny_matches_reference_golden(gpu, qtype, tag, norms):
     dev.close()
 
 
-@pytest.mark.parametrize("prompt_len", [2, 5, 6, 15, 20])
+@pytest.mark.parametrize("prompt_len", [2, 5, 6, 15, 29])
 def test_tinyllama_int4_prefill_step_chunk(gpu, tinyllama_int4, prompt_len):
-    """Prompts below the GEMM threshold (24 tokens) run as chunks of up to
-    15 consecutive tokens through the step kernels (each launch covers
-    every token of its chunk; the arithmetic per token is the decode
-    step's; from 6 tokens the row launches take four rows per wave; 20
-    tokens run as two chunks). Hidden state and K/V rows within rel-L2
-    1e-5 of the oracle's per-token prefill."""
+    """Prompts below the GEMM threshold (30 tokens) run as one chunk of
+    consecutive tokens through the step kernels (each launch covers every
+    token of the chunk; the arithmetic per token is the decode step's; from
+    6 tokens the row launches take four rows per wave). Hidden state and
+    K/V rows within rel-L2 1e-5 of the oracle's per-token prefill."""
     model, _, _, dev = tinyllama_int4
     prompt = gpu.synth_tokens(17, model.config.vocab_size, prompt_len)
     cache = gpu.KVCache(model.config)
@@ -471,14 +470,14 @@ def test_tinyllama_int4_prefill_step_chunk(gpu, tinyllama_int4, prompt_len):
 PREFILL_TOL = 2e-3  # rel-L2, batched (GEMM) prefill
 
 
-@pytest.mark.parametrize("prompt_len", [24, 40, 64, 130, 300])
+@pytest.mark.parametrize("prompt_len", [30, 40, 64, 130, 300])
 def test_tinyllama_int4_prefill_gemm(gpu, tinyllama_int4, prompt_len):
-    """Prompts of 24+ tokens run as a batch (MFMA GEMMs, causal attention).
+    """Prompts of 30+ tokens run as a batch (MFMA GEMMs, causal attention).
     Hidden state and K/V rows within rel-L2 2e-3 of the fp32 step arithmetic
-    (oracle for 24 and 40 tokens, the device step kernels for 64, 130 and
+    (oracle for 30 and 40 tokens, the device step kernels for 64, 130 and
     300: one whole 64-query attention tile with no padding, then three and
     five tiles), and the greedy ids that follow the prefill identical to the
-    oracle's. 24 tokens is the shortest batched prompt (40 padding rows in
+    oracle's. 30 tokens is the shortest batched prompt (34 padding rows in
     its tile)."""
     model, _, _, dev = tinyllama_int4
     prompt = gpu.synth_tokens(11, model.config.vocab_size, prompt_len)
