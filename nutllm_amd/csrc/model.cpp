@@ -190,18 +190,24 @@ void prefill_steps(nut_model &m, nut_kvcache &kv, size_t count)
 }
 
 // Prompts of at least this many tokens run as a batch (GEMM prefill);
-// shorter ones run as one step-kernel chunk (kStepTokensMax = 31).
-// TinyLlama INT4, batch against one chunk: 16 tokens 1.95 against 1.94 ms,
-// 24 tokens 3.11 against 2.64, 28 tokens 3.12 against 2.94, 31 tokens 3.12
-// against 3.16.
-constexpr size_t kPrefillGemmMin = 30;
+// shorter ones run as one step-kernel chunk (kStepTokensMax = 31). A chunk
+// costs its row dots once per token, the batch one 64-token MFMA tile, so
+// the crossover depends on the width. TinyLlama INT4 (dim 2048), batch
+// against one chunk: 24 tokens 3.11 against 2.64 ms, 28 tokens 3.12
+// against 2.94, 31 tokens 3.12 against 3.16. Llama-2-7B shape INT4 (dim
+// 4096): one chunk 4.78 ms at 8 tokens, 8.35 at 16, 13.9 at 29; the batch
+// 7.9 ms at 31.
+size_t prefill_gemm_min(const DecodeShape &s)
+{
+    return s.dim >= 4096 ? 16 : 30;
+}
 
 // The batched prefill applies when every layer uses 32-wide blocks, the
 // head size matches its attention tiles, and per-token steps are not
 // forced.
 bool use_prefill_gemm(const nut_model &m, size_t count)
 {
-    if (m.path == 1 || count < kPrefillGemmMin)
+    if (m.path == 1 || count < prefill_gemm_min(m.shape))
         return false;
     for (const DeviceLayer &l : m.layers)
         if (!prefill_gemm_supported(m.shape, l.view) || l.stage_scale[0] == nullptr)
